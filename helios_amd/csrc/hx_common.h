@@ -1,0 +1,83 @@
+// Shared device helpers for the gfx950 paged-KV kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/helios_paged.h"
+
+namespace hx {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// Element-type traits: 8-wide MFMA operand, the 16x16x32 MFMA, and conversions.
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<__bf16> {
+  typedef bf16x8_t v8;
+  static __device__ __forceinline__ f32x4_t mfma16x16x32(v8 a, v8 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  // Low / high 16-bit halves of a packed pair, widened to fp32 exactly.
+  static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  static __device__ __forceinline__ uint16_t bits(float f) {
+    __bf16 h = (__bf16)f;  // round to nearest even
+    return __builtin_bit_cast(uint16_t, h);
+  }
+};
+
+template <>
+struct Elem<_Float16> {
+  typedef f16x8_t v8;
+  static __device__ __forceinline__ f32x4_t mfma16x16x32(v8 a, v8 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+  }
+  static __device__ __forceinline__ float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+  static __device__ __forceinline__ uint16_t bits(float f) {
+    _Float16 h = (_Float16)f;
+    return __builtin_bit_cast(uint16_t, h);
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::v8 as_v8(uint4 u) {
+  return __builtin_bit_cast(typename Elem<T>::v8, u);
+}
+
+__device__ __forceinline__ uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
+
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
+  return (uint32_t)lo | ((uint32_t)hi << 16);
+}
+
+// Interleave the low (sel=0) or high (sel=1) 16-bit halves of x and y: {x.h, y.h}.
+__device__ __forceinline__ uint32_t interleave_lo(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t interleave_hi(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x07060302u);
+}
+
+__device__ __forceinline__ float wave_max_xor(float v, int mask_lo, int mask_hi) {
+  for (int m = mask_lo; m <= mask_hi; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_xor(float v, int mask_lo, int mask_hi) {
+  for (int m = mask_lo; m <= mask_hi; m <<= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+inline int status_from_hip(hipError_t e) { return e == hipSuccess ? HX_OK : (int)e; }
+
+}  // namespace hx

@@ -1,0 +1,291 @@
+// KV append, page copy and page gather for the paged KV pool (gfx950).
+//
+// All three are bit copies bound by HBM bandwidth. Each thread moves whole
+// 16-byte words where the sizes and alignments allow it (narrower words
+// otherwise), so a wavefront reads and writes full 128-byte lines.
+
+#include "hx_common.h"
+
+namespace {
+
+// ---------------------------------------------------------------- KV append
+// Reference: PagedBatchCache._write (src/helios/runtime/qwen3/paged_cache.py:335-345),
+// two index_copy_ calls along dim 0 of pool.view(-1, n_kv_heads, head_dim).
+struct AppendArgs {
+  uint8_t* k_pool;
+  uint8_t* v_pool;
+  const uint8_t* k;
+  const uint8_t* v;
+  const int64_t* slots;
+  int64_t pool_rows;
+  int64_t n_tokens;
+  int64_t k_row_b, k_head_b, v_row_b, v_head_b;  // byte strides of the new rows
+  int32_t n_kv;
+  int32_t head_b;   // bytes of one head row (head_dim * elem_bytes)
+  int32_t words;    // words of type W per head row
+};
+
+template <typename W>
+__global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
+  const int64_t per_token = (int64_t)a.n_kv * a.words;
+  const int64_t total = a.n_tokens * per_token;
+  const int64_t pool_row_b = (int64_t)a.n_kv * a.head_b;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = idx / per_token;
+    const int rem = (int)(idx - t * per_token);
+    const int h = rem / a.words;
+    const int w = rem - h * a.words;
+    const int64_t slot = a.slots[t];
+    if (slot < 0 || slot >= a.pool_rows) continue;
+    const int64_t dst = slot * pool_row_b + (int64_t)h * a.head_b;
+    const W kw = reinterpret_cast<const W*>(a.k + t * a.k_row_b + h * a.k_head_b)[w];
+    const W vw = reinterpret_cast<const W*>(a.v + t * a.v_row_b + h * a.v_head_b)[w];
+    reinterpret_cast<W*>(a.k_pool + dst)[w] = kw;
+    reinterpret_cast<W*>(a.v_pool + dst)[w] = vw;
+  }
+}
+
+// Largest word (16, 8, 4 or 2 bytes) dividing every size and address involved.
+int word_bytes_for(std::initializer_list<uint64_t> values) {
+  for (int w = 16; w >= 2; w >>= 1) {
+    bool ok = true;
+    for (uint64_t v : values) ok = ok && (v % (uint64_t)w == 0);
+    if (ok) return w;
+  }
+  return 1;
+}
+
+// ---------------------------------------------------------------- page copy
+// Reference semantics: KVCache.snapshot_block / restore_blocks
+// (src/helios/runtime/qwen3/cache.py:109-147): a bit-exact copy of a token block
+// for every layer, keys and values. Here the block is a set of whole pages.
+constexpr int kCopyMaxTensors = 64;   // K and V tensors per launch (32 layers)
+constexpr int kCopyMaxPages = 64;     // page pairs per launch
+constexpr int kCopyTileBytes = 64 * 1024;
+constexpr int kCopyThreads = 256;
+constexpr int kCopyIters = kCopyTileBytes / (kCopyThreads * 16);  // 16 x 16 B per thread
+
+struct CopyArgs {
+  uint8_t* tensors[kCopyMaxTensors];
+  int32_t src[kCopyMaxPages];
+  int32_t dst[kCopyMaxPages];
+  int64_t page_bytes;
+  int32_t n_tensors;
+  int32_t n_pages;
+  int32_t tiles_per_page;
+};
+
+__global__ __launch_bounds__(kCopyThreads) void kv_copy_pages_kernel(CopyArgs a) {
+  const int tile = blockIdx.x % a.tiles_per_page;
+  const int rest = blockIdx.x / a.tiles_per_page;
+  const int pair = rest % a.n_pages;
+  const int tensor = rest / a.n_pages;
+  uint8_t* base = a.tensors[tensor];
+  const uint8_t* src = base + (int64_t)a.src[pair] * a.page_bytes;
+  uint8_t* dst = base + (int64_t)a.dst[pair] * a.page_bytes;
+  const int64_t t0 = (int64_t)tile * kCopyTileBytes;
+  hx::u32x4_t buf[kCopyIters];
+#pragma unroll
+  for (int i = 0; i < kCopyIters; ++i) {
+    const int64_t off = t0 + ((int64_t)i * kCopyThreads + threadIdx.x) * 16;
+    buf[i] = off < a.page_bytes
+                 ? __builtin_nontemporal_load(reinterpret_cast<const hx::u32x4_t*>(src + off))
+                 : hx::u32x4_t{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int i = 0; i < kCopyIters; ++i) {
+    const int64_t off = t0 + ((int64_t)i * kCopyThreads + threadIdx.x) * 16;
+    if (off < a.page_bytes) __builtin_nontemporal_store(buf[i], reinterpret_cast<hx::u32x4_t*>(dst + off));
+  }
+}
+
+// ---------------------------------------------------------------- page gather
+// Reference: _gather_cpu (src/helios/runtime/qwen3/paged_cache.py:405-414).
+struct GatherArgs {
+  const uint8_t* pool;
+  const int32_t* pages;
+  uint8_t* out;
+  int64_t length;
+  int32_t num_pool_pages;
+  int32_t page_size;
+  int32_t n_kv;
+  int32_t head_b;
+  int32_t words;
+};
+
+template <typename W>
+__global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
+  const int64_t per_head = a.length * a.words;
+  const int64_t total = (int64_t)a.n_kv * per_head;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int h = (int)(idx / per_head);
+    const int64_t rem = idx - (int64_t)h * per_head;
+    const int64_t j = rem / a.words;
+    const int w = (int)(rem - j * a.words);
+    const int32_t page = a.pages[j / a.page_size];
+    W value;
+    if (page >= 0 && page < a.num_pool_pages) {
+      const int64_t row = (int64_t)page * a.page_size + j % a.page_size;
+      value = reinterpret_cast<const W*>(a.pool + (row * a.n_kv + h) * a.head_b)[w];
+    } else {
+      value = W{};
+    }
+    reinterpret_cast<W*>(a.out + idx / a.words * a.head_b)[w] = value;
+  }
+}
+
+int grid_for(int64_t items, int threads) {
+  int64_t blocks = (items + threads - 1) / threads;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 65536) blocks = 65536;
+  return (int)blocks;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* hx_strerror(int code) {
+  switch (code) {
+    case HX_OK: return "success";
+    case HX_E_INVALID_ARG: return "invalid argument";
+    case HX_E_UNSUPPORTED: return "unsupported head_dim, group size or dtype";
+    case HX_E_WORKSPACE: return "workspace missing, misaligned or too small";
+    case HX_E_OVERLAP: return "page copy sources and destinations overlap";
+    default: break;
+  }
+  if (code > 0) return hipGetErrorString((hipError_t)code);
+  return "unknown helios_paged status";
+}
+
+int hx_abi_version(void) { return 1; }
+
+int hx_kv_append(void* k_pool, void* v_pool, int64_t pool_rows,
+                 const void* k_new, int64_t k_row_stride, int64_t k_head_stride,
+                 const void* v_new, int64_t v_row_stride, int64_t v_head_stride,
+                 const int64_t* write_slots, int64_t n_tokens,
+                 int32_t n_kv_heads, int32_t head_dim, int32_t elem_bytes,
+                 void* stream) {
+  if (n_tokens < 0 || pool_rows < 0 || n_kv_heads < 1 || head_dim < 1) return HX_E_INVALID_ARG;
+  if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8) return HX_E_INVALID_ARG;
+  if (n_tokens == 0) return HX_OK;
+  if (!k_pool || !v_pool || !k_new || !v_new || !write_slots) return HX_E_INVALID_ARG;
+  AppendArgs a;
+  a.k_pool = static_cast<uint8_t*>(k_pool);
+  a.v_pool = static_cast<uint8_t*>(v_pool);
+  a.k = static_cast<const uint8_t*>(k_new);
+  a.v = static_cast<const uint8_t*>(v_new);
+  a.slots = write_slots;
+  a.pool_rows = pool_rows;
+  a.n_tokens = n_tokens;
+  a.k_row_b = k_row_stride * elem_bytes;
+  a.k_head_b = k_head_stride * elem_bytes;
+  a.v_row_b = v_row_stride * elem_bytes;
+  a.v_head_b = v_head_stride * elem_bytes;
+  a.n_kv = n_kv_heads;
+  a.head_b = head_dim * elem_bytes;
+  const int wb = word_bytes_for({(uint64_t)a.head_b, (uint64_t)a.k_row_b, (uint64_t)a.k_head_b,
+                                 (uint64_t)a.v_row_b, (uint64_t)a.v_head_b,
+                                 (uint64_t)(uintptr_t)k_pool, (uint64_t)(uintptr_t)v_pool,
+                                 (uint64_t)(uintptr_t)k_new, (uint64_t)(uintptr_t)v_new});
+  a.words = a.head_b / wb;
+  const int grid = grid_for(n_tokens * n_kv_heads * (int64_t)a.words, 256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (wb) {
+    case 16: hipLaunchKernelGGL(kv_append_kernel<uint4>, dim3(grid), dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL(kv_append_kernel<uint2>, dim3(grid), dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(kv_append_kernel<uint32_t>, dim3(grid), dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(kv_append_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(kv_append_kernel<uint8_t>, dim3(grid), dim3(256), 0, s, a); break;
+  }
+  return hx::status_from_hip(hipGetLastError());
+}
+
+int hx_kv_copy_pages(void* const* k_pools, void* const* v_pools, int32_t n_layers,
+                     const int32_t* src_pages, const int32_t* dst_pages, int32_t n_pages,
+                     int32_t num_pool_pages, int64_t page_bytes, void* stream) {
+  if (n_layers < 0 || n_pages < 0 || num_pool_pages < 1 || page_bytes < 16 || page_bytes % 16)
+    return HX_E_INVALID_ARG;
+  if (n_layers == 0 || n_pages == 0) return HX_OK;
+  if (!k_pools || !src_pages || !dst_pages) return HX_E_INVALID_ARG;
+  for (int i = 0; i < n_pages; ++i) {
+    if (src_pages[i] < 0 || src_pages[i] >= num_pool_pages) return HX_E_INVALID_ARG;
+    if (dst_pages[i] < 0 || dst_pages[i] >= num_pool_pages) return HX_E_INVALID_ARG;
+  }
+  for (int i = 0; i < n_pages; ++i)
+    for (int j = 0; j < n_pages; ++j) {
+      if (j > i && dst_pages[i] == dst_pages[j]) return HX_E_OVERLAP;
+      if (dst_pages[i] == src_pages[j]) return HX_E_OVERLAP;
+    }
+  const int per_layer = v_pools ? 2 : 1;
+  for (int l = 0; l < n_layers; ++l) {
+    if (!k_pools[l] || (v_pools && !v_pools[l])) return HX_E_INVALID_ARG;
+    if ((uintptr_t)k_pools[l] % 16 || (v_pools && (uintptr_t)v_pools[l] % 16)) return HX_E_INVALID_ARG;
+  }
+  const int tiles = (int)((page_bytes + kCopyTileBytes - 1) / kCopyTileBytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int total_tensors = n_layers * per_layer;
+  for (int t0 = 0; t0 < total_tensors; t0 += kCopyMaxTensors) {
+    const int nt = total_tensors - t0 < kCopyMaxTensors ? total_tensors - t0 : kCopyMaxTensors;
+    for (int p0 = 0; p0 < n_pages; p0 += kCopyMaxPages) {
+      const int np = n_pages - p0 < kCopyMaxPages ? n_pages - p0 : kCopyMaxPages;
+      CopyArgs a;
+      for (int t = 0; t < nt; ++t) {
+        const int flat = t0 + t;
+        const int layer = flat / per_layer;
+        a.tensors[t] = static_cast<uint8_t*>((flat % per_layer == 0) ? k_pools[layer] : v_pools[layer]);
+      }
+      for (int p = 0; p < np; ++p) {
+        a.src[p] = src_pages[p0 + p];
+        a.dst[p] = dst_pages[p0 + p];
+      }
+      a.page_bytes = page_bytes;
+      a.n_tensors = nt;
+      a.n_pages = np;
+      a.tiles_per_page = tiles;
+      const int64_t grid = (int64_t)nt * np * tiles;
+      hipLaunchKernelGGL(kv_copy_pages_kernel, dim3((unsigned)grid), dim3(kCopyThreads), 0, s, a);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return (int)e;
+    }
+  }
+  return HX_OK;
+}
+
+int hx_kv_gather(const void* pool, int32_t num_pool_pages, int32_t page_size,
+                 int32_t n_kv_heads, int32_t head_dim, int32_t elem_bytes,
+                 const int32_t* pages, int32_t n_pages, int64_t length,
+                 void* out, void* stream) {
+  if (num_pool_pages < 1 || page_size < 1 || n_kv_heads < 1 || head_dim < 1 || n_pages < 0 ||
+      length < 0)
+    return HX_E_INVALID_ARG;
+  if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8) return HX_E_INVALID_ARG;
+  if (length > (int64_t)n_pages * page_size) return HX_E_INVALID_ARG;
+  if (length == 0) return HX_OK;
+  if (!pool || !pages || !out) return HX_E_INVALID_ARG;
+  GatherArgs a;
+  a.pool = static_cast<const uint8_t*>(pool);
+  a.pages = pages;
+  a.out = static_cast<uint8_t*>(out);
+  a.length = length;
+  a.num_pool_pages = num_pool_pages;
+  a.page_size = page_size;
+  a.n_kv = n_kv_heads;
+  a.head_b = head_dim * elem_bytes;
+  const int wb = word_bytes_for({(uint64_t)a.head_b, (uint64_t)(uintptr_t)pool, (uint64_t)(uintptr_t)out});
+  a.words = a.head_b / wb;
+  const int grid = grid_for((int64_t)n_kv_heads * length * a.words, 256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (wb) {
+    case 16: hipLaunchKernelGGL(kv_gather_kernel<uint4>, dim3(grid), dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL(kv_gather_kernel<uint2>, dim3(grid), dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(kv_gather_kernel<uint32_t>, dim3(grid), dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(kv_gather_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(kv_gather_kernel<uint8_t>, dim3(grid), dim3(256), 0, s, a); break;
+  }
+  return hx::status_from_hip(hipGetLastError());
+}
+
+}  // extern "C"

@@ -1,0 +1,983 @@
+// Paged varlen GQA attention for gfx950 (MI355X).
+//
+// Replaces torch varlen_attn(..., block_table=..., seqused_k=..., window_size=(-1, 0))
+// as called by the reference at src/helios/runtime/qwen3/paged_cache.py:316-329 and
+// :506-519; its CPU restatement (the semantics matched here) is paged_cache.py:378-414
+// and :521-546.
+//
+// Kernels, all launched on the caller's stream:
+//   plan_kernel     one workgroup: validates the metadata, classifies every sequence as
+//                   a decode row (one query token) or a chunk (several), and writes the
+//                   work lists into the workspace. Run once per tick, reused per layer.
+//   decode_kernel   one workgroup per (256-key split, KV head). The G query heads of the
+//                   KV group share one read of the split's K and V (64 KiB each at
+//                   Qwen3-4B shape). QK^T runs on a 16x16x32 MFMA with the G heads as
+//                   rows; softmax uses wavefront xor-reductions plus a 4-wave LDS step;
+//                   PV runs on VALU with each 16-lane group streaming whole 256-byte V rows.
+//                   A sequence that fits one split writes its output directly; longer ones
+//                   write fp32 partials (m, l, o).
+//   combine_kernel  merges the partials of each long decode sequence in split order, so
+//                   results do not depend on scheduling.
+//   chunk_kernel    prefill chunks: 4 waves per workgroup, each wave owning 64 query rows
+//                   of one head; 64-key K / V^T tiles go through LDS with a register
+//                   prefetch of the next tile; S^T = K Q^T and O^T = V^T P^T both run on
+//                   16x16x32 MFMA with online softmax in between.
+
+#include "hx_common.h"
+
+#include <math.h>
+
+namespace {
+
+constexpr int kD = 128;          // head_dim built
+constexpr int kSplit = 256;      // keys per decode workgroup
+constexpr int kThreads = 256;    // 4 wavefronts
+constexpr int kTile = 64;        // keys per chunk-kernel tile
+constexpr int kPlanThreads = 1024;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Workspace header words.
+enum {
+  H_NDEC = 0, H_NPF = 1, H_NCOMB = 2, H_ERR = 3,
+  // shape the plan was built for; every run kernel checks it before using the lists
+  H_BATCH = 4, H_MAXQ = 5, H_MAXK = 6, H_HQ = 7, H_HKV = 8, H_STAMP = 9,
+  H_WORDS = 64
+};
+constexpr int kPlanStamp = 0x48585031;  // marks a header written by plan_kernel
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+struct Geometry {
+  int G, Gw, R, head_quads, rows_per_item;
+};
+
+inline Geometry geometry(int hq, int hkv) {
+  Geometry g;
+  g.G = hq / hkv;
+  g.Gw = g.G < 4 ? g.G : 4;
+  g.R = 4 / g.Gw;
+  g.head_quads = g.G / g.Gw;
+  g.rows_per_item = 64 * g.R;
+  return g;
+}
+
+struct Layout {
+  size_t seq_info, dec_items, comb_seqs, pf_items, part_ml, part_o, total;
+  int64_t max_dec, max_pf;
+};
+
+inline Layout make_layout(int batch, int max_q, int max_k, int hq, int hkv) {
+  const Geometry geo = geometry(hq, hkv);
+  Layout l;
+  const int64_t splits = max_k > 0 ? ceil_div(max_k, kSplit) : 1;
+  l.max_dec = (int64_t)batch * splits;
+  l.max_pf = max_q >= 2 ? (int64_t)batch * ceil_div(max_q, geo.rows_per_item) * geo.head_quads : 0;
+  size_t off = align256(H_WORDS * sizeof(int32_t));
+  l.seq_info = off;  off = align256(off + (size_t)batch * sizeof(int4));
+  l.dec_items = off; off = align256(off + (size_t)l.max_dec * sizeof(int4));
+  l.comb_seqs = off; off = align256(off + (size_t)batch * sizeof(int4));
+  l.pf_items = off;  off = align256(off + (size_t)l.max_pf * sizeof(int4));
+  l.part_ml = off;   off = align256(off + (size_t)l.max_dec * hq * sizeof(float2));
+  l.part_o = off;    off = align256(off + (size_t)l.max_dec * hq * kD * sizeof(float));
+  l.total = off;
+  return l;
+}
+
+// Decode key window of a one-token row at position L-1: keys [lo, L).
+__host__ __device__ inline int decode_lo(int L, int win_left) {
+  if (win_left < 0) return 0;
+  const int lo = L - 1 - win_left;
+  return lo > 0 ? lo : 0;
+}
+
+// Number of 256-key splits a decode row covers, and the first split. A row with no
+// keys still gets one (empty) split so its output row is written (zeros).
+__host__ __device__ inline void decode_splits(int L, int win_left, int* first, int* count) {
+  if (L <= 0) {
+    *first = 0;
+    *count = 1;
+    return;
+  }
+  const int lo = decode_lo(L, win_left);
+  *first = lo / kSplit;
+  *count = (L - 1) / kSplit - lo / kSplit + 1;
+}
+
+// ------------------------------------------------------------------ plan
+struct PlanArgs {
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  const int32_t* used_k;
+  int32_t* hdr;
+  int4* seq_info;
+  int4* dec_items;
+  int4* comb_seqs;
+  int4* pf_items;
+  int64_t total_k_rows;
+  int64_t max_dec, max_pf;
+  int32_t batch, total_q, max_q, max_k;
+  int32_t page_size, bt_stride;
+  int32_t rows_per_item, head_quads;
+  int32_t win_left, win_right;
+  int32_t hq, hkv;
+};
+
+__device__ int block_exclusive_scan(int v, int* wave_tot, int* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wave_tot[w] = x;
+  __syncthreads();
+  int pre = 0, tot = 0;
+  for (int i = 0; i < nw; ++i) {
+    const int t = wave_tot[i];
+    pre += i < w ? t : 0;
+    tot += t;
+  }
+  __syncthreads();
+  *total = tot;
+  return pre + x - v;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
+  __shared__ int wave_tot[kPlanThreads / 64];
+  __shared__ int err_bits;
+  if (threadIdx.x == 0) err_bits = 0;
+  __syncthreads();
+  int base_dec = 0, base_pf = 0, base_comb = 0;
+  int err = 0;
+  for (int b0 = 0; b0 < a.batch; b0 += kPlanThreads) {
+    const int b = b0 + (int)threadIdx.x;
+    const bool active = b < a.batch;
+    int q0 = 0, n = 0, L = 0, kvb = 0;
+    if (active) {
+      q0 = a.cu_q[b];
+      const int q1 = a.cu_q[b + 1];
+      if (q0 < 0 || q1 < q0 || q1 > a.total_q) {
+        err |= HX_WERR_BAD_CU_SEQ;
+        q0 = 0;
+        n = 0;
+      } else {
+        n = q1 - q0;
+      }
+      if (n > a.max_q) {
+        err |= HX_WERR_CLAMPED_LEN;
+        n = a.max_q;
+      }
+      if (a.used_k) {
+        L = a.used_k[b];
+      } else {
+        L = a.cu_k[b + 1] - a.cu_k[b];
+      }
+      if (L < 0) {
+        err |= HX_WERR_CLAMPED_LEN;
+        L = 0;
+      }
+      if (L > a.max_k) {
+        err |= HX_WERR_CLAMPED_LEN;
+        L = a.max_k;
+      }
+      if (a.page_size > 0) {
+        const int64_t cap = (int64_t)a.bt_stride * a.page_size;
+        if (L > cap) {
+          err |= HX_WERR_CLAMPED_LEN;
+          L = (int)cap;
+        }
+      } else {
+        kvb = a.cu_k[b];
+        if (kvb < 0 || kvb > a.total_k_rows) {
+          err |= HX_WERR_CLAMPED_LEN;
+          kvb = 0;
+          L = 0;
+        } else if ((int64_t)kvb + L > a.total_k_rows) {
+          err |= HX_WERR_CLAMPED_LEN;
+          L = (int)(a.total_k_rows - kvb);
+        }
+      }
+    }
+    int nd = 0, np = 0, nc = 0, s_first = 0, splits = 0, nblk = 0;
+    if (active && n == 1) {
+      decode_splits(L, a.win_left, &s_first, &splits);
+      nd = splits;
+      nc = splits > 1 ? 1 : 0;
+    } else if (active && n >= 2) {
+      nblk = (n + a.rows_per_item - 1) / a.rows_per_item;
+      np = nblk * a.head_quads;
+    }
+    int tot_d, tot_p, tot_c;
+    const int off_d = base_dec + block_exclusive_scan(nd, wave_tot, &tot_d);
+    const int off_p = base_pf + block_exclusive_scan(np, wave_tot, &tot_p);
+    const int off_c = base_comb + block_exclusive_scan(nc, wave_tot, &tot_c);
+    if (active) {
+      a.seq_info[b] = make_int4(q0, n, L, kvb);
+      for (int k = 0; k < nd; ++k) {
+        if (off_d + k < a.max_dec) a.dec_items[off_d + k] = make_int4(b, s_first + k, splits, off_d);
+      }
+      if (nc) a.comb_seqs[off_c] = make_int4(b, off_d, splits, 0);
+      // Later row blocks see more keys under a causal mask: list them first.
+      int k = 0;
+      for (int blk = nblk - 1; blk >= 0; --blk) {
+        for (int hq = 0; hq < a.head_quads; ++hq, ++k) {
+          if (off_p + k < a.max_pf) a.pf_items[off_p + k] = make_int4(b, blk * a.rows_per_item, hq, 0);
+        }
+      }
+    }
+    base_dec += tot_d;
+    base_pf += tot_p;
+    base_comb += tot_c;
+  }
+  if (err) atomicOr(&err_bits, err);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int e = err_bits;
+    if (base_dec > a.max_dec || base_pf > a.max_pf) e |= HX_WERR_GRID;
+    a.hdr[H_NDEC] = base_dec < a.max_dec ? base_dec : (int)a.max_dec;
+    a.hdr[H_NPF] = base_pf < a.max_pf ? base_pf : (int)a.max_pf;
+    a.hdr[H_NCOMB] = base_comb;
+    a.hdr[H_ERR] = e;
+    a.hdr[H_BATCH] = a.batch;
+    a.hdr[H_MAXQ] = a.max_q;
+    a.hdr[H_MAXK] = a.max_k;
+    a.hdr[H_HQ] = a.hq;
+    a.hdr[H_HKV] = a.hkv;
+    a.hdr[H_STAMP] = kPlanStamp;
+  }
+}
+
+// ------------------------------------------------------------------ run arguments
+struct RunArgs {
+  const uint8_t* q;
+  const uint8_t* k;
+  const uint8_t* v;
+  uint8_t* out;
+  float* lse;
+  const int32_t* bt;
+  int32_t* hdr;
+  const int4* seq_info;
+  const int4* dec_items;
+  const int4* comb_seqs;
+  const int4* pf_items;
+  float2* part_ml;
+  float* part_o;
+  int64_t q_row, q_head;     // element strides
+  int64_t kv_row, kv_head;
+  int64_t o_row, o_head;
+  int32_t num_pages, page_size, bt_stride;
+  int32_t batch, max_q, max_k;
+  int32_t total_q, hq, hkv;
+  float scale_log2;
+  int32_t win_left, win_right;
+  int32_t grid_dec, grid_pf, grid_comb;  // work items the launch grids cover
+};
+
+// True when the workspace holds a plan for this run's shape; otherwise the block
+// raises HX_WERR_PLAN_MISMATCH (once) and the caller must return without touching
+// the work lists.
+__device__ __forceinline__ bool plan_matches(const RunArgs& a) {
+  const int32_t* h = a.hdr;
+  const bool ok = h[H_STAMP] == kPlanStamp && h[H_BATCH] == a.batch && h[H_MAXQ] == a.max_q &&
+                  h[H_MAXK] == a.max_k && h[H_HQ] == a.hq && h[H_HKV] == a.hkv;
+  if (!ok && blockIdx.x == 0 && threadIdx.x == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_PLAN_MISMATCH);
+  return ok;
+}
+
+template <typename T>
+__device__ __forceinline__ uint4 ld16(const T* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+// ------------------------------------------------------------------ decode (split-K)
+template <typename T, int G>
+__global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
+  typedef hx::Elem<T> E;
+  constexpr int GP = G <= 4 ? 4 : 8;      // floats per token in p_lds
+  constexpr int NHG = (G + 3) / 4;        // 16-lane groups holding valid heads in the MFMA output
+  __shared__ __attribute__((aligned(16))) float p_lds[kSplit * GP];
+  __shared__ float red_max[4][16];
+  __shared__ float red_sum[4][16];
+  __shared__ float red_o[G * 8][kThreads];
+  __shared__ float fin_m[16];
+  __shared__ float fin_l[16];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int item = (int)blockIdx.x / a.hkv;
+  const int g = (int)blockIdx.x - item * a.hkv;
+  if (!plan_matches(a)) return;
+  const int n_dec = a.hdr[H_NDEC];
+  if (blockIdx.x == 0 && tid == 0 && n_dec > a.grid_dec) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
+  if (item >= n_dec) return;
+  const int4 it = a.dec_items[item];
+  const int b = it.x, s = it.y, splits = it.z;
+  if ((unsigned)b >= (unsigned)a.batch) return;
+  const int4 si = a.seq_info[b];
+  const int q0 = si.x, L = si.z;
+  const int key0 = s * kSplit;
+  const int kb = max(decode_lo(L, a.win_left), key0);
+  const int ke = min(L, key0 + kSplit);
+
+  int64_t row0;
+  bool page_ok = true;
+  if (a.page_size > 0) {
+    const int page = a.bt[(int64_t)b * a.bt_stride + key0 / a.page_size];
+    page_ok = page >= 0 && page < a.num_pages;
+    if (!page_ok && tid == 0 && kb < ke) atomicOr(&a.hdr[H_ERR], HX_WERR_BAD_PAGE);
+    row0 = (int64_t)(page_ok ? page : 0) * a.page_size + key0 % a.page_size;
+  } else {
+    row0 = (int64_t)si.w + key0;
+  }
+  const int kvr = (int)a.kv_row;
+  const T* kbase = reinterpret_cast<const T*>(a.k) + row0 * a.kv_row + (int64_t)g * a.kv_head;
+  const T* vbase = reinterpret_cast<const T*>(a.v) + row0 * a.kv_row + (int64_t)g * a.kv_head;
+
+  // K as the MFMA B operand: lane holds token 64w+16tb+(lane&15), dims 32st+8(lane>>4)..+7.
+  uint4 kf[4][4];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    const int n = 64 * w + 16 * tb + (lane & 15);
+    const bool ok = page_ok && key0 + n >= kb && key0 + n < ke;
+    const T* rp = kbase + n * kvr + 8 * (lane >> 4);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) kf[tb][st] = ok ? ld16(rp + 32 * st) : hx::zero4();
+  }
+  // V rows for the VALU PV: a 16-lane group covers one 256-byte row.
+  uint4 vr[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int n = 64 * w + 4 * i + (lane >> 4);
+    const bool ok = page_ok && key0 + n >= kb && key0 + n < ke;
+    vr[i] = ok ? ld16(vbase + n * kvr + 8 * (lane & 15)) : hx::zero4();
+  }
+  // q as the MFMA A operand: row = head (lane&15) of the group, zero rows beyond G.
+  uint4 qf[4];
+  {
+    const int m = lane & 15;
+    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)q0 * a.q_row +
+                  (int64_t)(g * G + (m < G ? m : 0)) * a.q_head + 8 * (lane >> 4);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) qf[st] = m < G ? ld16(qp + 32 * st) : hx::zero4();
+  }
+
+  // S = q K^T: lane holds heads 4(lane>>4)+i for token 16tb+(lane&15).
+  hx::f32x4_t sacc[4];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    sacc[tb] = hx::f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+      sacc[tb] = E::mfma16x16x32(hx::as_v8<T>(qf[st]), hx::as_v8<T>(kf[tb][st]), sacc[tb]);
+  }
+
+  const int hg = lane >> 4;
+  float sc[4][4];
+  float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    const int key = key0 + 64 * w + 16 * tb + (lane & 15);
+    const bool ok = page_ok && key >= kb && key < ke;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc[tb][i] = ok ? sacc[tb][i] * a.scale_log2 : -INFINITY;
+      mx[i] = fmaxf(mx[i], sc[tb][i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) mx[i] = hx::wave_max_xor(mx[i], 1, 8);
+  if ((lane & 15) == 0 && hg < NHG) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red_max[w][4 * hg + i] = mx[i];
+  }
+  __syncthreads();
+  float m[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -INFINITY;
+    if (hg < NHG) {
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) m[i] = fmaxf(m[i], red_max[ww][4 * hg + i]);
+    }
+  }
+  float ps[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = sc[tb][i] == -INFINITY ? 0.f : exp2f(sc[tb][i] - m[i]);
+      sc[tb][i] = p;
+      ps[i] += p;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ps[i] = hx::wave_sum_xor(ps[i], 1, 8);
+  if ((lane & 15) == 0 && hg < NHG) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red_sum[w][4 * hg + i] = ps[i];
+  }
+  if (hg < NHG) {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      const int n = 64 * w + 16 * tb + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (4 * hg + i < G) p_lds[n * GP + 4 * hg + i] = sc[tb][i];
+    }
+  }
+  __syncthreads();
+
+  // O = P V on VALU, fp32 accumulate.
+  float o[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+  const int r = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int n = 64 * w + 4 * i + r;
+    float pv[GP];
+#pragma unroll
+    for (int j = 0; j < GP; j += 4) {
+      const float4 t4 = *reinterpret_cast<const float4*>(&p_lds[n * GP + j]);
+      pv[j] = t4.x;
+      pv[j + 1] = t4.y;
+      pv[j + 2] = t4.z;
+      pv[j + 3] = t4.w;
+    }
+    const uint4 vv = vr[i];
+    const float vf[8] = {E::lo(vv.x), E::hi(vv.x), E::lo(vv.y), E::hi(vv.y),
+                         E::lo(vv.z), E::hi(vv.z), E::lo(vv.w), E::hi(vv.w)};
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[h][e] = fmaf(pv[h], vf[e], o[h][e]);
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red_o[h * 8 + e][tid] = o[h][e];
+  if (tid < G) {
+    float mm = -INFINITY, ll = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      mm = fmaxf(mm, red_max[ww][tid]);
+      ll += red_sum[ww][tid];
+    }
+    fin_m[tid] = mm;
+    fin_l[tid] = ll;
+  }
+  __syncthreads();
+
+  for (int oi = tid; oi < G * kD; oi += kThreads) {
+    const int h = oi >> 7, d = oi & (kD - 1), c = d >> 3, e = d & 7;
+    float acc = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) acc += red_o[h * 8 + e][ww * 64 + rr * 16 + c];
+    const float mh = fin_m[h], lh = fin_l[h];
+    const int qh = g * G + h;
+    if (splits == 1) {
+      const float val = lh > 0.f ? acc / lh : 0.f;
+      reinterpret_cast<uint16_t*>(a.out)[(int64_t)q0 * a.o_row + (int64_t)qh * a.o_head + d] = E::bits(val);
+      if (a.lse && d == 0)
+        a.lse[(int64_t)qh * a.total_q + q0] = lh > 0.f ? (mh + log2f(lh)) * kLn2 : -INFINITY;
+    } else {
+      a.part_o[((int64_t)item * a.hq + qh) * kD + d] = acc;
+      if (d == 0) a.part_ml[(int64_t)item * a.hq + qh] = make_float2(mh, lh);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ split combine
+template <typename T, int G>
+__global__ __launch_bounds__(kThreads) void combine_kernel(RunArgs a) {
+  typedef hx::Elem<T> E;
+  const int cs = (int)blockIdx.x / a.hkv;
+  const int g = (int)blockIdx.x - cs * a.hkv;
+  if (!plan_matches(a)) return;
+  const int n_comb = a.hdr[H_NCOMB];
+  if (blockIdx.x == 0 && threadIdx.x == 0 && n_comb > a.grid_comb) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
+  if (cs >= n_comb) return;
+  const int4 c = a.comb_seqs[cs];
+  const int first = c.y, splits = c.z;
+  if ((unsigned)c.x >= (unsigned)a.batch || first < 0 || splits < 1) return;
+  if ((int64_t)first + splits > (int64_t)a.hdr[H_NDEC]) return;
+  const int q0 = a.seq_info[c.x].x;
+  for (int oi = threadIdx.x; oi < G * kD; oi += kThreads) {
+    const int h = oi >> 7, d = oi & (kD - 1);
+    const int qh = g * G + h;
+    float M = -INFINITY;
+    for (int s = 0; s < splits; ++s) M = fmaxf(M, a.part_ml[(int64_t)(first + s) * a.hq + qh].x);
+    float lsum = 0.f, acc = 0.f;
+    for (int s = 0; s < splits; ++s) {
+      const float2 ml = a.part_ml[(int64_t)(first + s) * a.hq + qh];
+      const float wgt = ml.x == -INFINITY ? 0.f : exp2f(ml.x - M);
+      lsum += wgt * ml.y;
+      acc += wgt * a.part_o[((int64_t)(first + s) * a.hq + qh) * kD + d];
+    }
+    const float val = lsum > 0.f ? acc / lsum : 0.f;
+    reinterpret_cast<uint16_t*>(a.out)[(int64_t)q0 * a.o_row + (int64_t)qh * a.o_head + d] = E::bits(val);
+    if (a.lse && d == 0)
+      a.lse[(int64_t)qh * a.total_q + q0] = lsum > 0.f ? (M + log2f(lsum)) * kLn2 : -INFINITY;
+  }
+}
+
+// ------------------------------------------------------------------ chunk (prefill) MFMA
+constexpr int kKStride = kD + 8;       // K tile row: 136 elements (272 B)
+constexpr int kVStride = kTile + 4;    // V^T tile row: 68 elements (136 B)
+
+template <typename T, int G>
+__global__ __launch_bounds__(kThreads, 1) void chunk_kernel(RunArgs a) {
+  typedef hx::Elem<T> E;
+  typedef typename E::v8 v8;
+  constexpr int Gw = G < 4 ? G : 4;
+  constexpr int R = 4 / Gw;
+  __shared__ __attribute__((aligned(16))) T k_lds[kTile * kKStride];
+  __shared__ __attribute__((aligned(16))) T vt_lds[kD * kVStride];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int item = (int)blockIdx.x / a.hkv;
+  const int g = (int)blockIdx.x - item * a.hkv;
+  if (!plan_matches(a)) return;
+  const int n_pf = a.hdr[H_NPF];
+  if (blockIdx.x == 0 && tid == 0 && n_pf > a.grid_pf) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
+  if (item >= n_pf) return;
+  const int4 it = a.pf_items[item];
+  const int b = it.x, row0 = it.y, hquad = it.z;
+  if ((unsigned)b >= (unsigned)a.batch) return;
+  const int4 si = a.seq_info[b];
+  const int q0 = si.x, n = si.y, L = si.z, kvb = si.w;
+  const int off = L - n;  // key position of query row 0
+  const int wg_row_end = min(n, row0 + 64 * R);
+
+  int klo = 0;
+  if (a.win_left >= 0) klo = max(0, off + row0 - a.win_left);
+  int khi = L - 1;
+  if (a.win_right >= 0) khi = min(khi, off + wg_row_end - 1 + a.win_right);
+  const int t_begin = klo / kTile;
+  const int t_end = khi >= klo ? khi / kTile + 1 : t_begin;
+
+  const int wr0 = row0 + 64 * (w / Gw);
+  const int qh = g * G + hquad * Gw + (w % Gw);
+
+  // Q^T as the MFMA B operand: lane holds row wr0+16rb+(lane&15), dims 32st+8(lane>>4)..+7.
+  uint4 qf[4][4];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    const int rr = wr0 + 16 * rb + (lane & 15);
+    const bool ok = rr < n;
+    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)(q0 + (ok ? rr : 0)) * a.q_row +
+                  (int64_t)qh * a.q_head + 8 * (lane >> 4);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) qf[rb][st] = ok ? ld16(qp + 32 * st) : hx::zero4();
+  }
+
+  hx::f32x4_t oacc[8][4];
+#pragma unroll
+  for (int db = 0; db < 8; ++db)
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) oacc[db][rb] = hx::f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  float l_run[4] = {0.f, 0.f, 0.f, 0.f};
+
+  const int c16 = tid & 15;     // 16-byte chunk of a key row this thread moves
+  const int kr_base = tid >> 4; // 0..15
+
+  uint4 kreg[4], vreg[4];
+  auto load_tile = [&](int t) {
+    const int key_base = t * kTile;
+    int64_t rowb;
+    bool ok_page = true;
+    if (a.page_size > 0) {
+      const int page = a.bt[(int64_t)b * a.bt_stride + key_base / a.page_size];
+      ok_page = page >= 0 && page < a.num_pages;
+      if (!ok_page && tid == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_BAD_PAGE);
+      rowb = (int64_t)(ok_page ? page : 0) * a.page_size + key_base % a.page_size;
+    } else {
+      rowb = (int64_t)kvb + key_base;
+    }
+    const T* kp = reinterpret_cast<const T*>(a.k) + rowb * a.kv_row + (int64_t)g * a.kv_head + 8 * c16;
+    const T* vp = reinterpret_cast<const T*>(a.v) + rowb * a.kv_row + (int64_t)g * a.kv_head + 8 * c16;
+    const int kvr = (int)a.kv_row;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int kk = kr_base + 16 * j;
+      kreg[j] = (ok_page && key_base + kk < L) ? ld16(kp + kk * kvr) : hx::zero4();
+      const int vk = 2 * kr_base + (j & 1) + 32 * (j >> 1);
+      vreg[j] = (ok_page && key_base + vk < L) ? ld16(vp + vk * kvr) : hx::zero4();
+    }
+  };
+
+  if (t_begin < t_end) load_tile(t_begin);
+  for (int t = t_begin; t < t_end; ++t) {
+    // Registers -> LDS: K row-major, V transposed (pairs of keys packed per 32-bit word).
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<uint4*>(&k_lds[(kr_base + 16 * j) * kKStride + 8 * c16]) = kreg[j];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const uint4 x = vreg[2 * jj], y = vreg[2 * jj + 1];
+      const int kp2 = 2 * kr_base + 32 * jj;
+      const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+      const uint32_t ys[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+      for (int wd = 0; wd < 4; ++wd) {
+        const int d = 8 * c16 + 2 * wd;
+        *reinterpret_cast<uint32_t*>(&vt_lds[d * kVStride + kp2]) = hx::interleave_lo(xs[wd], ys[wd]);
+        *reinterpret_cast<uint32_t*>(&vt_lds[(d + 1) * kVStride + kp2]) = hx::interleave_hi(xs[wd], ys[wd]);
+      }
+    }
+    __syncthreads();
+    if (t + 1 < t_end) load_tile(t + 1);
+
+    const int t0 = t * kTile;
+    // S^T = K Q^T: lane holds keys 16kb+4(lane>>4)+i of row 16rb+(lane&15).
+    hx::f32x4_t sacc[4][4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) sacc[kb][rb] = hx::f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const uint4 af = *reinterpret_cast<const uint4*>(
+            &k_lds[(16 * kb + (lane & 15)) * kKStride + 32 * st + 8 * (lane >> 4)]);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+          sacc[kb][rb] = E::mfma16x16x32(hx::as_v8<T>(af), hx::as_v8<T>(qf[rb][st]), sacc[kb][rb]);
+      }
+    }
+
+    // Mask only where the tile is not fully visible to every row of this wave.
+    bool full = (n - wr0 >= 64) && (t0 + kTile - 1 <= L - 1);
+    if (a.win_left >= 0) full = full && (off + wr0 + 63 - a.win_left <= t0);
+    if (a.win_right >= 0) full = full && (off + wr0 + a.win_right >= t0 + kTile - 1);
+
+    v8 pb[2][4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const int rr = wr0 + 16 * rb + (lane & 15);
+      const int qpos = off + rr;
+      int rlo = a.win_left >= 0 ? qpos - a.win_left : -2147483647;
+      int rhi = L - 1;
+      if (a.win_right >= 0) rhi = min(rhi, qpos + a.win_right);
+      if (rr >= n) rhi = -1;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float v = sacc[kb][rb][i] * a.scale_log2;
+          if (!full) {
+            const int key = t0 + 16 * kb + 4 * (lane >> 4) + i;
+            if (key < rlo || key > rhi) v = -INFINITY;
+          }
+          sacc[kb][rb][i] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run[rb], mx);
+      const float alpha = m_new == -INFINITY ? 1.f : exp2f(m_run[rb] - m_new);
+      float psum = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = m_new == -INFINITY ? 0.f : exp2f(sacc[kb][rb][i] - m_new);
+          sacc[kb][rb][i] = p;
+          psum += p;
+        }
+      l_run[rb] = l_run[rb] * alpha + psum;
+      m_run[rb] = m_new;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) oacc[db][rb] *= alpha;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        uint16_t h8[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          h8[e] = E::bits(sacc[2 * ks][rb][e]);
+          h8[e + 4] = E::bits(sacc[2 * ks + 1][rb][e]);
+        }
+        const uint4 u = make_uint4(hx::pack2(h8[0], h8[1]), hx::pack2(h8[2], h8[3]),
+                                   hx::pack2(h8[4], h8[5]), hx::pack2(h8[6], h8[7]));
+        pb[ks][rb] = hx::as_v8<T>(u);
+      }
+    }
+
+    // O^T += V^T P^T with the key order of pb: {4(lane>>4)+0..3, 16+4(lane>>4)+0..3}.
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const T* vrow = &vt_lds[(16 * db + (lane & 15)) * kVStride + 32 * ks + 4 * (lane >> 4)];
+        const uint2 lo8 = *reinterpret_cast<const uint2*>(vrow);
+        const uint2 hi8 = *reinterpret_cast<const uint2*>(vrow + 16);
+        const v8 af = hx::as_v8<T>(make_uint4(lo8.x, lo8.y, hi8.x, hi8.y));
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) oacc[db][rb] = E::mfma16x16x32(af, pb[ks][rb], oacc[db][rb]);
+      }
+    }
+    __syncthreads();
+  }
+
+  // Normalise and store: lane holds dims 16db+4(lane>>4)+0..3 of row 16rb+(lane&15).
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    float l = l_run[rb];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const int rr = wr0 + 16 * rb + (lane & 15);
+    if (rr < n) {
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + (int64_t)(q0 + rr) * a.o_row + (int64_t)qh * a.o_head;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        const int d0 = 16 * db + 4 * (lane >> 4);
+        const uint2 u = make_uint2(hx::pack2(E::bits(oacc[db][rb][0] * inv), E::bits(oacc[db][rb][1] * inv)),
+                                   hx::pack2(E::bits(oacc[db][rb][2] * inv), E::bits(oacc[db][rb][3] * inv)));
+        *reinterpret_cast<uint2*>(orow + d0) = u;
+      }
+      if (a.lse && (lane >> 4) == 0)
+        a.lse[(int64_t)qh * a.total_q + q0 + rr] = l > 0.f ? (m_run[rb] + log2f(l)) * kLn2 : -INFINITY;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ host helpers
+bool valid_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
+
+template <typename T, int G>
+int launch_run(const RunArgs& a, hipStream_t s) {
+  if (a.grid_dec > 0)
+    hipLaunchKernelGGL((decode_kernel<T, G>), dim3((unsigned)(a.grid_dec * a.hkv)), dim3(kThreads), 0, s, a);
+  if (a.grid_comb > 0)
+    hipLaunchKernelGGL((combine_kernel<T, G>), dim3((unsigned)(a.grid_comb * a.hkv)), dim3(kThreads), 0, s, a);
+  if (a.grid_pf > 0)
+    hipLaunchKernelGGL((chunk_kernel<T, G>), dim3((unsigned)(a.grid_pf * a.hkv)), dim3(kThreads), 0, s, a);
+  return hx::status_from_hip(hipGetLastError());
+}
+
+template <typename T>
+int launch_run_g(const RunArgs& a, int G, hipStream_t s) {
+  switch (G) {
+    case 1: return launch_run<T, 1>(a, s);
+    case 2: return launch_run<T, 2>(a, s);
+    case 4: return launch_run<T, 4>(a, s);
+    case 8: return launch_run<T, 8>(a, s);
+    default: return HX_E_UNSUPPORTED;
+  }
+}
+
+int check_shape(int batch, int max_q, int max_k, int hq, int hkv, int head_dim) {
+  if (batch < 0 || max_q < 0 || max_k < 0 || hq < 1 || hkv < 1) return HX_E_INVALID_ARG;
+  if (hq % hkv) return HX_E_INVALID_ARG;
+  if (!valid_group(hq / hkv) || head_dim != kD) return HX_E_UNSUPPORTED;
+  return HX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t hx_varlen_attn_workspace_bytes(int32_t batch, int32_t max_q, int32_t max_k,
+                                      int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim) {
+  if (check_shape(batch, max_q, max_k, n_q_heads, n_kv_heads, head_dim) != HX_OK) return 0;
+  return make_layout(batch, max_q, max_k, n_q_heads, n_kv_heads).total;
+}
+
+size_t hx_varlen_attn_error_word_offset(void) { return H_ERR * sizeof(int32_t); }
+
+int hx_varlen_attn_count_items(const int32_t* q_lens, const int32_t* k_lens, int32_t batch,
+                               int32_t n_q_heads, int32_t n_kv_heads,
+                               int32_t window_left, int32_t window_right,
+                               int32_t* decode_items, int32_t* prefill_items,
+                               int32_t* combine_seqs) {
+  (void)window_right;
+  if (batch < 0 || n_q_heads < 1 || n_kv_heads < 1 || n_q_heads % n_kv_heads) return HX_E_INVALID_ARG;
+  if (batch > 0 && (!q_lens || !k_lens)) return HX_E_INVALID_ARG;
+  if (!decode_items || !prefill_items || !combine_seqs) return HX_E_INVALID_ARG;
+  const Geometry geo = geometry(n_q_heads, n_kv_heads);
+  int64_t nd = 0, np = 0, nc = 0;
+  for (int b = 0; b < batch; ++b) {
+    const int n = q_lens[b], L = k_lens[b];
+    if (n < 0 || L < 0) return HX_E_INVALID_ARG;
+    if (n == 1) {
+      int first, count;
+      decode_splits(L, window_left, &first, &count);
+      nd += count;
+      nc += count > 1;
+    } else if (n >= 2) {
+      np += ceil_div(n, geo.rows_per_item) * geo.head_quads;
+    }
+  }
+  if (nd > INT32_MAX || np > INT32_MAX) return HX_E_INVALID_ARG;
+  *decode_items = (int32_t)nd;
+  *prefill_items = (int32_t)np;
+  *combine_seqs = (int32_t)nc;
+  return HX_OK;
+}
+
+int hx_varlen_attn_plan(const int32_t* cu_seq_q, const int32_t* cu_seq_k,
+                        const int32_t* seqused_k, int32_t batch, int32_t total_q,
+                        int32_t max_q, int32_t max_k, int64_t total_k_rows,
+                        int32_t page_size, int32_t block_table_stride,
+                        int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                        int32_t window_left, int32_t window_right,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  int st = check_shape(batch, max_q, max_k, n_q_heads, n_kv_heads, head_dim);
+  if (st != HX_OK) return st;
+  if (total_q < 0 || page_size < 0 || (page_size > 0 && page_size % kSplit)) return HX_E_INVALID_ARG;
+  if (page_size > 0 && block_table_stride < 1) return HX_E_INVALID_ARG;
+  if (page_size == 0 && (!cu_seq_k || total_k_rows < 0)) return HX_E_INVALID_ARG;
+  if (batch > 0 && !cu_seq_q) return HX_E_INVALID_ARG;
+  if (batch > 0 && !seqused_k && !cu_seq_k) return HX_E_INVALID_ARG;
+  const Layout l = make_layout(batch, max_q, max_k, n_q_heads, n_kv_heads);
+  if (!workspace || (uintptr_t)workspace % 256 || workspace_bytes < l.total) return HX_E_WORKSPACE;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const Geometry geo = geometry(n_q_heads, n_kv_heads);
+  PlanArgs a;
+  a.cu_q = cu_seq_q;
+  a.cu_k = cu_seq_k;
+  a.used_k = seqused_k;
+  a.hdr = reinterpret_cast<int32_t*>(ws);
+  a.seq_info = reinterpret_cast<int4*>(ws + l.seq_info);
+  a.dec_items = reinterpret_cast<int4*>(ws + l.dec_items);
+  a.comb_seqs = reinterpret_cast<int4*>(ws + l.comb_seqs);
+  a.pf_items = reinterpret_cast<int4*>(ws + l.pf_items);
+  a.total_k_rows = total_k_rows;
+  a.max_dec = l.max_dec;
+  a.max_pf = l.max_pf;
+  a.batch = batch;
+  a.total_q = total_q;
+  a.max_q = max_q;
+  a.max_k = max_k;
+  a.page_size = page_size;
+  a.bt_stride = block_table_stride;
+  a.rows_per_item = geo.rows_per_item;
+  a.head_quads = geo.head_quads;
+  a.win_left = window_left;
+  a.win_right = window_right;
+  a.hq = n_q_heads;
+  a.hkv = n_kv_heads;
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, static_cast<hipStream_t>(stream), a);
+  return hx::status_from_hip(hipGetLastError());
+}
+
+int hx_varlen_attn_run(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                       const void* k_cache, const void* v_cache,
+                       int64_t kv_row_stride, int64_t kv_head_stride,
+                       int32_t num_pages, int32_t page_size,
+                       const int32_t* block_table, int32_t block_table_stride,
+                       int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                       int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                       float scale, int32_t window_left, int32_t window_right,
+                       int32_t dtype,
+                       void* out, int64_t o_row_stride, int64_t o_head_stride,
+                       float* lse,
+                       int32_t decode_items_hint, int32_t prefill_items_hint,
+                       int32_t combine_seqs_hint,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  int st = check_shape(batch, max_q, max_k, n_q_heads, n_kv_heads, head_dim);
+  if (st != HX_OK) return st;
+  if (dtype != HX_DTYPE_BF16 && dtype != HX_DTYPE_FP16) return HX_E_UNSUPPORTED;
+  if (total_q < 0 || page_size < 0 || (page_size > 0 && page_size % kSplit)) return HX_E_INVALID_ARG;
+  if (page_size > 0 && (num_pages < 1 || block_table_stride < 1 || !block_table)) return HX_E_INVALID_ARG;
+  if (!(scale > 0.f) || !isfinite(scale)) return HX_E_INVALID_ARG;
+  // 16-byte vector loads of q / K / V rows and 8-byte stores of output rows.
+  if (!q || !k_cache || !v_cache || !out) return batch == 0 ? HX_OK : HX_E_INVALID_ARG;
+  if ((uintptr_t)q % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16 || (uintptr_t)out % 8)
+    return HX_E_INVALID_ARG;
+  if (q_row_stride % 8 || q_head_stride % 8 || kv_row_stride % 8 || kv_head_stride % 8 ||
+      o_row_stride % 4 || o_head_stride % 4)
+    return HX_E_INVALID_ARG;
+  if (q_row_stride < 0 || q_head_stride < 0 || kv_row_stride < 0 || kv_head_stride < 0 ||
+      o_row_stride < 0 || o_head_stride < 0)
+    return HX_E_INVALID_ARG;
+  // Per-split row offsets are 32-bit: 256 rows of kv_row_stride must fit.
+  if (kv_row_stride > (int64_t)(1 << 23)) return HX_E_INVALID_ARG;
+  const Layout l = make_layout(batch, max_q, max_k, n_q_heads, n_kv_heads);
+  if (!workspace || (uintptr_t)workspace % 256 || workspace_bytes < l.total) return HX_E_WORKSPACE;
+  if (batch == 0) return HX_OK;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  RunArgs a;
+  a.q = static_cast<const uint8_t*>(q);
+  a.k = static_cast<const uint8_t*>(k_cache);
+  a.v = static_cast<const uint8_t*>(v_cache);
+  a.out = static_cast<uint8_t*>(out);
+  a.lse = lse;
+  a.bt = block_table;
+  a.hdr = reinterpret_cast<int32_t*>(ws);
+  a.seq_info = reinterpret_cast<const int4*>(ws + l.seq_info);
+  a.dec_items = reinterpret_cast<const int4*>(ws + l.dec_items);
+  a.comb_seqs = reinterpret_cast<const int4*>(ws + l.comb_seqs);
+  a.pf_items = reinterpret_cast<const int4*>(ws + l.pf_items);
+  a.part_ml = reinterpret_cast<float2*>(ws + l.part_ml);
+  a.part_o = reinterpret_cast<float*>(ws + l.part_o);
+  a.q_row = q_row_stride;
+  a.q_head = q_head_stride;
+  a.kv_row = kv_row_stride;
+  a.kv_head = kv_head_stride;
+  a.o_row = o_row_stride;
+  a.o_head = o_head_stride;
+  a.num_pages = num_pages;
+  a.page_size = page_size;
+  a.bt_stride = block_table_stride;
+  a.batch = batch;
+  a.max_q = max_q;
+  a.max_k = max_k;
+  a.total_q = total_q;
+  a.hq = n_q_heads;
+  a.hkv = n_kv_heads;
+  a.scale_log2 = scale * kLog2e;
+  a.win_left = window_left;
+  a.win_right = window_right;
+  auto clamp_hint = [](int32_t hint, int64_t bound) -> int32_t {
+    if (hint < 0 || hint > bound) return (int32_t)bound;
+    return hint;
+  };
+  a.grid_dec = clamp_hint(decode_items_hint, l.max_dec);
+  a.grid_pf = max_q >= 2 ? clamp_hint(prefill_items_hint, l.max_pf) : 0;
+  a.grid_comb = clamp_hint(combine_seqs_hint, batch);
+  if ((int64_t)a.grid_dec * n_kv_heads > INT32_MAX || (int64_t)a.grid_pf * n_kv_heads > INT32_MAX)
+    return HX_E_INVALID_ARG;
+  const int G = n_q_heads / n_kv_heads;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == HX_DTYPE_BF16) return launch_run_g<__bf16>(a, G, s);
+  return launch_run_g<_Float16>(a, G, s);
+}
+
+int hx_varlen_attn(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                   const void* k_cache, const void* v_cache,
+                   int64_t kv_row_stride, int64_t kv_head_stride,
+                   int32_t num_pages, int32_t page_size,
+                   const int32_t* block_table, int32_t block_table_stride,
+                   const int32_t* cu_seq_q, const int32_t* cu_seq_k,
+                   const int32_t* seqused_k,
+                   int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                   int64_t total_k_rows,
+                   int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                   float scale, int32_t window_left, int32_t window_right,
+                   int32_t dtype,
+                   void* out, int64_t o_row_stride, int64_t o_head_stride,
+                   float* lse,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  int st = hx_varlen_attn_plan(cu_seq_q, cu_seq_k, seqused_k, batch, total_q, max_q, max_k,
+                               total_k_rows, page_size, block_table_stride, n_q_heads, n_kv_heads,
+                               head_dim, window_left, window_right, workspace, workspace_bytes, stream);
+  if (st != HX_OK) return st;
+  return hx_varlen_attn_run(q, q_row_stride, q_head_stride, k_cache, v_cache, kv_row_stride,
+                            kv_head_stride, num_pages, page_size, block_table, block_table_stride,
+                            batch, total_q, max_q, max_k, n_q_heads, n_kv_heads, head_dim, scale,
+                            window_left, window_right, dtype, out, o_row_stride, o_head_stride, lse,
+                            -1, -1, -1, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,416 @@
+"""Python call surface of the MI355X paged-KV hot path.
+
+``varlen_attn`` keeps the keyword surface the reference uses at
+src/helios/runtime/qwen3/paged_cache.py:316-329 and :506-519
+(torch 2.13 ``torch.nn.attention.varlen.varlen_attn`` with ``block_table=``), so
+that module can import it in place of torch's. ``kv_append``, ``kv_copy_pages`` and
+``kv_gather`` replace ``PagedBatchCache._write`` (paged_cache.py:335-345),
+``KVCache.restore_blocks``' copy (cache.py:131-147) and ``_gather_cpu``
+(paged_cache.py:405-414).
+
+Every function validates its arguments on the host (ValueError, like
+``_validate_attention_inputs`` at paged_cache.py:352-375), allocates outputs and
+workspaces with ``torch.empty`` on the query's device (the caching allocator owns
+them), and launches on ``torch.cuda.current_stream()`` without synchronising.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from collections.abc import Sequence
+from typing import NamedTuple
+
+import torch
+
+from helios_amd import _capi
+
+_SUPPORTED = {torch.bfloat16: _capi.HX_DTYPE_BF16, torch.float16: _capi.HX_DTYPE_FP16}
+
+
+class AuxRequest(NamedTuple):
+    """Auxiliary outputs of varlen_attn (same field as torch's AuxRequest)."""
+
+    lse: bool = False
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(*tensors: torch.Tensor) -> torch.device:
+    device = tensors[0].device
+    if device.type != "cuda":
+        raise RuntimeError(
+            "helios_amd kernels run on a ROCm device only; got tensors on "
+            f"{device}. There is no CPU fallback."
+        )
+    for t in tensors[1:]:
+        if t.device != device:
+            raise ValueError("All tensors must be on the same device.")
+    return device
+
+
+def _elem_bytes(t: torch.Tensor) -> int:
+    return t.element_size()
+
+
+# --------------------------------------------------------------------- KV append
+def kv_append(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    write_slots: torch.Tensor,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+) -> None:
+    """``k_cache.view(-1, Hkv, d).index_copy_(0, write_slots, keys)``, same for V.
+
+    ``k_cache``/``v_cache``: pool tensors whose trailing dims are ``[Hkv, d]`` and
+    that are contiguous (``[num_pages, page_size, Hkv, d]`` in the reference).
+    ``keys``/``values``: ``[T, Hkv, d]`` with a contiguous last dim (any row/head
+    strides). ``write_slots``: int64 ``[T]`` flat slot ids (page * page_size + offset).
+    """
+    device = _require_gpu(k_cache, v_cache, write_slots, keys, values)
+    if k_cache.shape != v_cache.shape or k_cache.dtype != v_cache.dtype:
+        raise ValueError("Key and value pools must have identical shapes and dtypes.")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("KV pools must be contiguous.")
+    if keys.ndim != 3 or values.shape != keys.shape:
+        raise ValueError("Appended keys and values must be [tokens, kv_heads, head_dim].")
+    n_kv, head_dim = keys.shape[1], keys.shape[2]
+    if tuple(k_cache.shape[-2:]) != (n_kv, head_dim):
+        raise ValueError("Appended K/V heads do not match the pool layout.")
+    if keys.dtype != k_cache.dtype or values.dtype != k_cache.dtype:
+        raise ValueError("Appended K/V dtype must match the pool dtype.")
+    if write_slots.dtype != torch.int64 or write_slots.ndim != 1 or write_slots.shape[0] != keys.shape[0]:
+        raise ValueError("write_slots must be int64 [tokens].")
+    if keys.stride(2) != 1 or values.stride(2) != 1:
+        raise ValueError("Appended K/V must have a contiguous head_dim.")
+    write_slots = write_slots.contiguous()
+    pool_rows = k_cache.numel() // (n_kv * head_dim)
+    code = _capi.lib().hx_kv_append(
+        k_cache.data_ptr(), v_cache.data_ptr(), pool_rows,
+        keys.data_ptr(), keys.stride(0), keys.stride(1),
+        values.data_ptr(), values.stride(0), values.stride(1),
+        write_slots.data_ptr(), keys.shape[0],
+        n_kv, head_dim, _elem_bytes(keys),
+        _stream_ptr(device),
+    )
+    _capi.check(code, "hx_kv_append")
+
+
+# --------------------------------------------------------------------- page copy
+def kv_copy_pages(
+    k_caches: Sequence[torch.Tensor],
+    v_caches: Sequence[torch.Tensor] | None,
+    src_pages: Sequence[int],
+    dst_pages: Sequence[int],
+) -> None:
+    """Copy whole pages for every layer: ``cache[l][dst[i]] = cache[l][src[i]]``.
+
+    Bit-exact; the page-granular form of KVCache.snapshot_block/restore_blocks
+    (cache.py:109-147). ``src_pages``/``dst_pages`` are host lists; destinations
+    must be distinct and disjoint from the sources.
+    """
+    if len(src_pages) != len(dst_pages):
+        raise ValueError("Source and destination page lists differ in length.")
+    if not k_caches:
+        return
+    tensors = list(k_caches) + (list(v_caches) if v_caches is not None else [])
+    device = _require_gpu(*tensors)
+    shape, dtype = k_caches[0].shape, k_caches[0].dtype
+    if v_caches is not None and len(v_caches) != len(k_caches):
+        raise ValueError("Key and value layer lists differ in length.")
+    for t in tensors:
+        if t.shape != shape or t.dtype != dtype or not t.is_contiguous():
+            raise ValueError("Every pool tensor must share one contiguous [pages, ...] layout.")
+    n_layers, n_pages = len(k_caches), len(src_pages)
+    if n_pages == 0:
+        return
+    page_bytes = k_caches[0][0].numel() * k_caches[0].element_size()
+    k_ptrs = (ctypes.c_void_p * n_layers)(*[t.data_ptr() for t in k_caches])
+    v_ptrs = (
+        (ctypes.c_void_p * n_layers)(*[t.data_ptr() for t in v_caches])
+        if v_caches is not None
+        else None
+    )
+    src = (ctypes.c_int32 * n_pages)(*[int(p) for p in src_pages])
+    dst = (ctypes.c_int32 * n_pages)(*[int(p) for p in dst_pages])
+    code = _capi.lib().hx_kv_copy_pages(
+        k_ptrs, v_ptrs, n_layers, src, dst, n_pages, shape[0], page_bytes, _stream_ptr(device)
+    )
+    _capi.check(code, "hx_kv_copy_pages")
+
+
+# --------------------------------------------------------------------- page gather
+def kv_gather(cache: torch.Tensor, pages: torch.Tensor | Sequence[int], length: int) -> torch.Tensor:
+    """Paged -> dense ``[1, Hkv, length, d]`` (``_gather_cpu``, paged_cache.py:405-414)."""
+    device = _require_gpu(cache)
+    if cache.ndim != 4 or not cache.is_contiguous():
+        raise ValueError("cache must be a contiguous [pages, page_size, kv_heads, head_dim] pool.")
+    num_pages, page_size, n_kv, head_dim = cache.shape
+    if not isinstance(pages, torch.Tensor):
+        pages = torch.tensor(list(pages), dtype=torch.int32, device=device)
+    if pages.ndim != 1 or pages.dtype != torch.int32 or pages.device != device:
+        raise ValueError("pages must be an int32 vector on the cache's device.")
+    pages = pages.contiguous()
+    if length < 0 or length > pages.shape[0] * page_size:
+        raise ValueError("length exceeds the listed pages.")
+    out = torch.empty((1, n_kv, length, head_dim), dtype=cache.dtype, device=device)
+    code = _capi.lib().hx_kv_gather(
+        cache.data_ptr(), num_pages, page_size, n_kv, head_dim, cache.element_size(),
+        pages.data_ptr(), pages.shape[0], length, out.data_ptr(), _stream_ptr(device),
+    )
+    _capi.check(code, "hx_kv_gather")
+    return out
+
+
+# --------------------------------------------------------------------- attention
+def _window(window_size, is_causal: bool) -> tuple[int, int]:
+    if window_size is None:
+        return (-1, 0) if is_causal else (-1, -1)
+    left, right = (int(x) for x in window_size)
+    if is_causal:
+        right = 0 if right < 0 else min(right, 0)
+    return left, right
+
+
+def workspace_bytes(batch: int, max_q: int, max_k: int, n_q_heads: int, n_kv_heads: int, head_dim: int) -> int:
+    nbytes = _capi.lib().hx_varlen_attn_workspace_bytes(batch, max_q, max_k, n_q_heads, n_kv_heads, head_dim)
+    if nbytes == 0:
+        raise ValueError(
+            "Unsupported attention shape: head_dim must be 128 and n_q_heads / n_kv_heads "
+            "one of 1, 2, 4, 8."
+        )
+    return nbytes
+
+
+def count_items(q_lens: Sequence[int], k_lens: Sequence[int], n_q_heads: int, n_kv_heads: int,
+                window: tuple[int, int]) -> tuple[int, int, int]:
+    """Exact work-item counts the device planner will produce for these lengths."""
+    batch = len(q_lens)
+    ql = (ctypes.c_int32 * max(batch, 1))(*q_lens)
+    kl = (ctypes.c_int32 * max(batch, 1))(*k_lens)
+    nd, np_, nc = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    code = _capi.lib().hx_varlen_attn_count_items(
+        ql, kl, batch, n_q_heads, n_kv_heads, window[0], window[1],
+        ctypes.byref(nd), ctypes.byref(np_), ctypes.byref(nc),
+    )
+    _capi.check(code, "hx_varlen_attn_count_items")
+    return nd.value, np_.value, nc.value
+
+
+class VarlenAttnPlan:
+    """Work plan for one set of varlen metadata, reusable across layers.
+
+    Built once per tick (the reference's metadata is identical for all 36 layers),
+    then ``run`` is called per layer. ``q_lens``/``k_lens`` (host lists), when given,
+    size the launch grids exactly; otherwise the bounds from (batch, max_q, max_k)
+    are used and surplus workgroups exit at once.
+    """
+
+    def __init__(
+        self,
+        cu_seq_q: torch.Tensor,
+        cu_seq_k: torch.Tensor | None,
+        seqused_k: torch.Tensor | None,
+        *,
+        total_q: int,
+        max_q: int,
+        max_k: int,
+        n_q_heads: int,
+        n_kv_heads: int,
+        head_dim: int,
+        page_size: int,
+        block_table_stride: int,
+        total_k_rows: int = 0,
+        window: tuple[int, int] = (-1, 0),
+        q_lens: Sequence[int] | None = None,
+        k_lens: Sequence[int] | None = None,
+    ) -> None:
+        device = _require_gpu(cu_seq_q)
+        for name, t in (("cu_seq_q", cu_seq_q), ("cu_seq_k", cu_seq_k), ("seqused_k", seqused_k)):
+            if t is None:
+                continue
+            if t.dtype != torch.int32 or t.ndim != 1 or t.device != device:
+                raise ValueError(f"{name} must be an int32 vector on the query's device.")
+        batch = cu_seq_q.shape[0] - 1
+        if batch < 0:
+            raise ValueError("cu_seq_q must have batch + 1 entries.")
+        if cu_seq_k is not None and cu_seq_k.shape[0] != batch + 1:
+            raise ValueError("cu_seq_k must have batch + 1 entries.")
+        if seqused_k is not None and seqused_k.shape[0] != batch:
+            raise ValueError("seqused_k must have batch entries.")
+        if seqused_k is None and cu_seq_k is None:
+            raise ValueError("Either seqused_k or cu_seq_k is required.")
+        if max_q < 0 or max_k < 0:
+            raise ValueError("max_q and max_k must be non-negative.")
+        self.device = device
+        self.batch = batch
+        self.total_q = total_q
+        self.max_q = max_q
+        self.max_k = max_k
+        self.n_q_heads = n_q_heads
+        self.n_kv_heads = n_kv_heads
+        self.head_dim = head_dim
+        self.page_size = page_size
+        self.block_table_stride = block_table_stride
+        self.window = window
+        self._metadata = (cu_seq_q.contiguous(), None if cu_seq_k is None else cu_seq_k.contiguous(),
+                          None if seqused_k is None else seqused_k.contiguous())
+        self.ws_bytes = workspace_bytes(max(batch, 0), max_q, max_k, n_q_heads, n_kv_heads, head_dim)
+        self.workspace = torch.empty(self.ws_bytes + 256, dtype=torch.uint8, device=device)
+        base = self.workspace.data_ptr()
+        self._ws_offset = (-base) % 256
+        self.ws_ptr = base + self._ws_offset
+        if q_lens is not None and k_lens is not None:
+            self.hints = count_items(q_lens, k_lens, n_q_heads, n_kv_heads, window)
+        else:
+            self.hints = (-1, -1, -1)
+        cu_q, cu_k, used = self._metadata
+        code = _capi.lib().hx_varlen_attn_plan(
+            cu_q.data_ptr(),
+            None if cu_k is None else cu_k.data_ptr(),
+            None if used is None else used.data_ptr(),
+            batch, total_q, max_q, max_k, total_k_rows, page_size, block_table_stride,
+            n_q_heads, n_kv_heads, head_dim, window[0], window[1],
+            self.ws_ptr, self.ws_bytes, _stream_ptr(device),
+        )
+        _capi.check(code, "hx_varlen_attn_plan")
+
+    def error_word(self) -> int:
+        """HX_WERR_* bits raised so far (synchronises the device to read them)."""
+        off = self._ws_offset + _capi.lib().hx_varlen_attn_error_word_offset()
+        return int(self.workspace[off:off + 4].view(torch.int32).item())
+
+    def run(
+        self,
+        query: torch.Tensor,
+        k_cache: torch.Tensor,
+        v_cache: torch.Tensor,
+        block_table: torch.Tensor | None,
+        *,
+        scale: float | None = None,
+        out: torch.Tensor | None = None,
+        return_lse: bool = False,
+    ) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
+        _require_gpu(query, k_cache, v_cache)
+        if query.device != self.device:
+            raise ValueError("Query is not on the plan's device.")
+        if query.dtype not in _SUPPORTED:
+            raise ValueError("varlen_attn supports bfloat16 and float16 queries.")
+        if query.ndim != 3 or query.shape[0] != self.total_q or query.shape[1] != self.n_q_heads \
+                or query.shape[2] != self.head_dim:
+            raise ValueError("Query must be [total_q, n_q_heads, head_dim] as planned.")
+        if k_cache.shape != v_cache.shape or k_cache.dtype != query.dtype or v_cache.dtype != query.dtype:
+            raise ValueError("Key/value caches must match each other and the query dtype.")
+        if k_cache.stride() != v_cache.stride():
+            raise ValueError("Key and value caches must share strides.")
+        if self.page_size > 0:
+            if k_cache.ndim != 4 or k_cache.shape[1] != self.page_size:
+                raise ValueError("Paged caches must be [num_pages, page_size, kv_heads, head_dim].")
+            if block_table is None or block_table.dtype != torch.int32 or block_table.ndim != 2 \
+                    or block_table.shape[0] != self.batch or block_table.device != self.device:
+                raise ValueError("block_table must be int32 [batch, width] on the query's device.")
+            if block_table.stride(1) != 1 or block_table.shape[1] != self.block_table_stride \
+                    or block_table.stride(0) != self.block_table_stride:
+                raise ValueError("block_table must be row-contiguous with the planned width.")
+            num_pages = k_cache.shape[0]
+            row_stride, head_stride = k_cache.stride(1), k_cache.stride(2)
+            if k_cache.stride(0) != self.page_size * row_stride:
+                raise ValueError("Pages must be laid out back to back.")
+        else:
+            if k_cache.ndim != 3:
+                raise ValueError("Packed caches must be [total_k, kv_heads, head_dim].")
+            num_pages = 0
+            row_stride, head_stride = k_cache.stride(0), k_cache.stride(1)
+        if k_cache.shape[-2] != self.n_kv_heads or k_cache.shape[-1] != self.head_dim or k_cache.stride(-1) != 1:
+            raise ValueError("Key/value caches must be [..., n_kv_heads, head_dim] with contiguous head_dim.")
+        if query.stride(2) != 1:
+            query = query.contiguous()
+        if out is None:
+            out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+        elif out.shape != query.shape or out.dtype != query.dtype or out.stride(2) != 1:
+            raise ValueError("out must match the query's shape and dtype.")
+        lse = None
+        if return_lse:
+            lse = torch.empty((self.n_q_heads, self.total_q), dtype=torch.float32, device=query.device)
+        scale = 1.0 / math.sqrt(self.head_dim) if scale is None else float(scale)
+        code = _capi.lib().hx_varlen_attn_run(
+            query.data_ptr(), query.stride(0), query.stride(1),
+            k_cache.data_ptr(), v_cache.data_ptr(), row_stride, head_stride,
+            num_pages, self.page_size,
+            None if block_table is None else block_table.data_ptr(), self.block_table_stride,
+            self.batch, self.total_q, self.max_q, self.max_k,
+            self.n_q_heads, self.n_kv_heads, self.head_dim,
+            scale, self.window[0], self.window[1], _SUPPORTED[query.dtype],
+            out.data_ptr(), out.stride(0), out.stride(1),
+            None if lse is None else lse.data_ptr(),
+            self.hints[0], self.hints[1], self.hints[2],
+            self.ws_ptr, self.ws_bytes, _stream_ptr(query.device),
+        )
+        _capi.check(code, "hx_varlen_attn_run")
+        return (out, lse) if return_lse else out
+
+
+def varlen_attn(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    cu_seq_q: torch.Tensor,
+    cu_seq_k: torch.Tensor | None,
+    max_q: int,
+    max_k: int,
+    is_causal: bool = False,
+    return_aux: AuxRequest | None = None,
+    *,
+    window_size: tuple[int, int] | None = None,
+    enable_gqa: bool = False,
+    seqused_k: torch.Tensor | None = None,
+    block_table: torch.Tensor | None = None,
+    num_splits: int | None = None,
+    scale: float | None = None,
+) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
+    """Drop-in for the paged ``varlen_attn`` call at paged_cache.py:316-329 / :506-519.
+
+    ``query``: ``[total_q, Hq, d]``. With ``block_table`` (int32 ``[B, W]``),
+    ``key``/``value`` are pools ``[num_pages, page_size, Hkv, d]`` and sequence b
+    has ``seqused_k[b]`` keys (else ``cu_seq_k[b+1]-cu_seq_k[b]``); without it they
+    are packed ``[total_k, Hkv, d]`` located by ``cu_seq_k``. ``window_size=(-1, 0)``
+    is the bottom-right causal mask. ``num_splits`` is accepted for signature parity:
+    the split schedule is fixed by each sequence's length, and the combine order is
+    fixed, so results are deterministic for any value.
+    """
+    del num_splits
+    device = _require_gpu(query, key, value, cu_seq_q)
+    if query.ndim != 3:
+        raise ValueError("query must be [total_q, n_q_heads, head_dim].")
+    n_q_heads, head_dim = query.shape[1], query.shape[2]
+    n_kv_heads = key.shape[-2]
+    if n_q_heads != n_kv_heads and not enable_gqa:
+        raise ValueError("Query and KV head counts differ; pass enable_gqa=True.")
+    if n_kv_heads < 1 or n_q_heads % n_kv_heads:
+        raise ValueError("Query heads must be a multiple of KV heads for GQA.")
+    window = _window(window_size, is_causal)
+    paged = block_table is not None
+    if paged:
+        page_size = key.shape[1]
+        bt_stride = block_table.shape[1] if block_table.ndim == 2 else 0
+        if block_table.stride(-1) != 1:
+            block_table = block_table.contiguous()
+        total_k_rows = 0
+    else:
+        if cu_seq_k is None:
+            raise ValueError("Packed keys need cu_seq_k.")
+        page_size, bt_stride = 0, 0
+        total_k_rows = key.shape[0]
+    plan = VarlenAttnPlan(
+        cu_seq_q, cu_seq_k, seqused_k,
+        total_q=query.shape[0], max_q=max_q, max_k=max_k,
+        n_q_heads=n_q_heads, n_kv_heads=n_kv_heads, head_dim=head_dim,
+        page_size=page_size, block_table_stride=bt_stride, total_k_rows=total_k_rows,
+        window=window,
+    )
+    want_lse = bool(return_aux is not None and return_aux.lse)
+    del device
+    return plan.run(query, key, value, block_table, scale=scale, return_lse=want_lse)

@@ -1,0 +1,203 @@
+/*
+ * helios_paged.h — C ABI of the MI355X paged-KV hot path.
+ *
+ * Three operations, matching the reference's paged KV cache
+ * (src/helios/runtime/qwen3/paged_cache.py) and its dense-KV block copy
+ * (src/helios/runtime/qwen3/cache.py):
+ *   - KV append into a shared pool of pages           (hx_kv_append)
+ *   - page-table-driven varlen GQA attention         (hx_varlen_attn*)
+ *   - prefix block restore / page copy and gather    (hx_kv_copy_pages, hx_kv_gather)
+ *
+ * Conventions
+ *   - Every pointer named *_pool, *_cache, q, k_new, v_new, out, lse, workspace,
+ *     write_slots, pages, block_table, cu_seq_*, seqused_k is a DEVICE pointer
+ *     unless the comment says "host".
+ *   - Strides are in ELEMENTS, and the innermost (head_dim) dimension is contiguous.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *   - Calls are asynchronous and stream-ordered. The library never synchronises
+ *     the device, never allocates device memory, and keeps no state between calls.
+ *   - Return value: 0 on success; a negative HX_E* code for an argument error
+ *     (the caller maps it to ValueError); a positive hipError_t for a launch error.
+ *     Nothing throws or aborts across this ABI.
+ *   - Device-side metadata (write slots, page ids, sequence lengths) is clamped or
+ *     skipped when out of range, so no kernel reads or writes outside the buffers
+ *     it was given; hx_varlen_attn_* also raise bits in the workspace error word.
+ *
+ * Pool layout (paged_cache.py:47-55): one K and one V tensor per layer, each
+ *   [num_pages, page_size, n_kv_heads, head_dim], contiguous. Page id p addresses
+ *   pool[p]; block tables are int32 [batch, width], padded with page 0.
+ */
+#ifndef HELIOS_PAGED_H
+#define HELIOS_PAGED_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------------- */
+#define HX_OK 0
+#define HX_E_INVALID_ARG (-1)   /* a size, stride, pointer or id is out of range   */
+#define HX_E_UNSUPPORTED (-2)   /* head_dim / group size / dtype not built         */
+#define HX_E_WORKSPACE (-3)     /* workspace missing, misaligned or too small      */
+#define HX_E_OVERLAP (-4)       /* page copy source and destination sets overlap   */
+
+/* ---- element types -------------------------------------------------------- */
+#define HX_DTYPE_BF16 0
+#define HX_DTYPE_FP16 1
+
+/* ---- bits of the workspace error word (hx_varlen_attn_error_word) --------- */
+#define HX_WERR_BAD_PAGE 1        /* a block-table entry outside [0, num_pages)     */
+#define HX_WERR_CLAMPED_LEN 2     /* a sequence length above max_k / max_q / table  */
+#define HX_WERR_BAD_CU_SEQ 4      /* cu_seq_q not monotone or beyond total_q        */
+#define HX_WERR_GRID 8            /* more work items than the launch grid covered   */
+#define HX_WERR_PLAN_MISMATCH 16  /* run called with a shape its plan was not built for */
+
+/* Human-readable text for a status code (static storage). */
+const char* hx_strerror(int code);
+
+/* ABI version: bumped on any signature change. */
+int hx_abi_version(void);
+
+/*
+ * KV append (replaces PagedBatchCache._write, paged_cache.py:335-345, i.e. two
+ * index_copy_ calls on pool.view(-1, n_kv_heads, head_dim)):
+ *   for t in [0, n_tokens): k_pool_rows[write_slots[t]] = k_new[t]
+ *                           v_pool_rows[write_slots[t]] = v_new[t]
+ * where a pool row is n_kv_heads * head_dim contiguous elements and pool_rows =
+ * num_pages * page_size. k_new[t][h] starts at k_new + t*k_row_stride + h*k_head_stride.
+ * Slots outside [0, pool_rows) are skipped. Duplicate slots: last writer is unspecified
+ * (as for index_copy_). Bit-exact copy of elem_bytes-wide elements.
+ */
+int hx_kv_append(void* k_pool, void* v_pool, int64_t pool_rows,
+                 const void* k_new, int64_t k_row_stride, int64_t k_head_stride,
+                 const void* v_new, int64_t v_row_stride, int64_t v_head_stride,
+                 const int64_t* write_slots, int64_t n_tokens,
+                 int32_t n_kv_heads, int32_t head_dim, int32_t elem_bytes,
+                 void* stream);
+
+/*
+ * Page copy across layers (the page-granular form of KVCache.snapshot_block /
+ * restore_blocks, cache.py:109-147, which copy a block of tokens for every layer,
+ * K and V, bit-exactly; and of PagedKVCache.restore_blocks, paged_cache.py:142-163,
+ * when the restored pages must be private copies):
+ *   for l < n_layers, i < n_pages:  k_pools[l][dst_pages[i]] = k_pools[l][src_pages[i]]
+ *                                   v_pools[l][dst_pages[i]] = v_pools[l][src_pages[i]]
+ * k_pools / v_pools are HOST arrays of n_layers device pointers (v_pools may be NULL
+ * to copy K only); src_pages / dst_pages are HOST arrays of n_pages page ids.
+ * page_bytes = page_size * n_kv_heads * head_dim * elem_bytes. Destination ids must
+ * be distinct and disjoint from the sources (HX_E_OVERLAP otherwise).
+ */
+int hx_kv_copy_pages(void* const* k_pools, void* const* v_pools, int32_t n_layers,
+                     const int32_t* src_pages, const int32_t* dst_pages, int32_t n_pages,
+                     int32_t num_pool_pages, int64_t page_bytes, void* stream);
+
+/*
+ * Page gather paged -> dense (replaces _gather_cpu, paged_cache.py:405-414:
+ * index_select over pages, flatten, keep the first `length` tokens, permute to
+ * head-major):  out[h][j][:] = pool[pages[j / page_size]][j % page_size][h][:]
+ * for j < length; out is [n_kv_heads, length, head_dim] contiguous. pages is a
+ * DEVICE array of n_pages int32 ids; an id outside [0, num_pool_pages) yields zeros.
+ */
+int hx_kv_gather(const void* pool, int32_t num_pool_pages, int32_t page_size,
+                 int32_t n_kv_heads, int32_t head_dim, int32_t elem_bytes,
+                 const int32_t* pages, int32_t n_pages, int64_t length,
+                 void* out, void* stream);
+
+/*
+ * Paged varlen GQA attention (replaces torch varlen_attn(q, k_cache, v_cache,
+ * cu_seq_q, cu_seq_k, max_q, max_k, window_size=(-1, 0), enable_gqa=...,
+ * seqused_k=..., block_table=..., num_splits=1) at paged_cache.py:316-329 and
+ * :506-519). For sequence b with query rows cu_seq_q[b]..cu_seq_q[b+1] (n_b rows)
+ * and L_b keys (seqused_k[b], or cu_seq_k[b+1]-cu_seq_k[b] when seqused_k is NULL),
+ * row i sits at key position qpos = L_b - n_b + i (bottom-right aligned) and sees
+ * keys j with  (window_left  < 0 or j >= qpos - window_left) and
+ *              (window_right < 0 or j <= qpos + window_right) and j < L_b.
+ * Query head h reads KV head h / (n_q_heads / n_kv_heads).
+ *   O[row, h] = softmax_j(scale * q[row, h] . K[j, h/G]) @ V[j, h/G]
+ * Keys live in pages when page_size > 0: key j of sequence b is row
+ * block_table[b * block_table_stride + j / page_size] * page_size + j % page_size
+ * of the pool viewed as [num_pages * page_size, n_kv_heads, head_dim]. When
+ * page_size == 0 the keys are packed: key j of b is row cu_seq_k[b] + j of a
+ * [total_k_rows, n_kv_heads, head_dim] tensor (block_table ignored).
+ * A row with no visible key outputs zeros (lse = -inf).
+ * Built for head_dim 128, n_q_heads / n_kv_heads in {1, 2, 4, 8}, bf16 and fp16;
+ * softmax and accumulation in fp32.
+ *
+ * Work split: decode rows (n_b == 1) run a split-K kernel, one workgroup per
+ * (256-key split, KV head) whose 4 query heads share each K/V read, and a
+ * deterministic combine; chunk rows (n_b > 1) run a bf16/fp16 MFMA kernel.
+ *
+ * The workspace (size from hx_varlen_attn_workspace_bytes, 256-byte aligned) holds
+ * the work plan and the split-K partials. hx_varlen_attn_plan writes the plan from
+ * the metadata; hx_varlen_attn_run consumes it and may be called any number of
+ * times (e.g. once per layer) while cu_seq_q / cu_seq_k / seqused_k and the scalar
+ * shape arguments are unchanged. hx_varlen_attn = plan + run.
+ *
+ * decode_items_hint / prefill_items_hint size the launch grids. Pass -1 to use the
+ * bound derived from (batch, max_q, max_k); a caller that knows the host-side
+ * lengths passes the exact counts from hx_varlen_attn_count_items to avoid empty
+ * workgroups. A hint below the real count sets HX_WERR_GRID (rows left unwritten).
+ */
+size_t hx_varlen_attn_workspace_bytes(int32_t batch, int32_t max_q, int32_t max_k,
+                                      int32_t n_q_heads, int32_t n_kv_heads,
+                                      int32_t head_dim);
+
+/* Host-side item counts for known lengths (q_lens[b] = n_b, k_lens[b] = L_b, HOST
+ * arrays); mirrors the device planner exactly. Returns 0 or HX_E_INVALID_ARG. */
+int hx_varlen_attn_count_items(const int32_t* q_lens, const int32_t* k_lens, int32_t batch,
+                               int32_t n_q_heads, int32_t n_kv_heads,
+                               int32_t window_left, int32_t window_right,
+                               int32_t* decode_items, int32_t* prefill_items,
+                               int32_t* combine_seqs);
+
+int hx_varlen_attn_plan(const int32_t* cu_seq_q, const int32_t* cu_seq_k,
+                        const int32_t* seqused_k, int32_t batch, int32_t total_q,
+                        int32_t max_q, int32_t max_k, int64_t total_k_rows,
+                        int32_t page_size, int32_t block_table_stride,
+                        int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                        int32_t window_left, int32_t window_right,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+int hx_varlen_attn_run(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                       const void* k_cache, const void* v_cache,
+                       int64_t kv_row_stride, int64_t kv_head_stride,
+                       int32_t num_pages, int32_t page_size,
+                       const int32_t* block_table, int32_t block_table_stride,
+                       int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                       int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                       float scale, int32_t window_left, int32_t window_right,
+                       int32_t dtype,
+                       void* out, int64_t o_row_stride, int64_t o_head_stride,
+                       float* lse,
+                       int32_t decode_items_hint, int32_t prefill_items_hint,
+                       int32_t combine_seqs_hint,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+int hx_varlen_attn(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                   const void* k_cache, const void* v_cache,
+                   int64_t kv_row_stride, int64_t kv_head_stride,
+                   int32_t num_pages, int32_t page_size,
+                   const int32_t* block_table, int32_t block_table_stride,
+                   const int32_t* cu_seq_q, const int32_t* cu_seq_k,
+                   const int32_t* seqused_k,
+                   int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                   int64_t total_k_rows,
+                   int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                   float scale, int32_t window_left, int32_t window_right,
+                   int32_t dtype,
+                   void* out, int64_t o_row_stride, int64_t o_head_stride,
+                   float* lse,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* Byte offset of the int32 error word inside the workspace (OR of HX_WERR_* bits,
+ * cleared by each hx_varlen_attn_plan). */
+size_t hx_varlen_attn_error_word_offset(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HELIOS_PAGED_H */

@@ -1,0 +1,105 @@
+"""The C ABI library loads and exports every declared symbol; host-only entry
+points behave (no GPU work is launched here)."""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import subprocess
+
+import pytest
+
+from helios_amd import _capi, ops, synth
+
+
+def test_library_exports_every_header_function():
+    names = _capi.header_functions()
+    assert len(names) == len(set(names)) >= 10
+    assert set(names) == set(_capi.SIGNATURES), "binding table out of sync with the header"
+    lib = _capi.lib()
+    for name in names:
+        assert getattr(lib, name) is not None
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_capi.LIBRARY_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    assert set(names) <= exported
+
+
+def test_abi_version_and_strerror():
+    assert _capi.lib().hx_abi_version() == 1
+    assert _capi.strerror(0) == "success"
+    assert "invalid" in _capi.strerror(_capi.HX_E_INVALID_ARG)
+    with pytest.raises(ValueError):
+        _capi.check(_capi.HX_E_UNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        _capi.check(1, "x")
+
+
+def test_workspace_bytes_supported_shapes():
+    lib = _capi.lib()
+    assert lib.hx_varlen_attn_workspace_bytes(64, 1, 4097, 32, 8, 128) > 0
+    assert lib.hx_varlen_attn_workspace_bytes(64, 1, 4097, 32, 8, 64) == 0   # head_dim
+    assert lib.hx_varlen_attn_workspace_bytes(64, 1, 4097, 48, 8, 128) == 0  # G = 6
+    assert lib.hx_varlen_attn_workspace_bytes(64, 1, 4097, 30, 8, 128) == 0  # not a multiple
+    with pytest.raises(ValueError):
+        ops.workspace_bytes(1, 1, 1, 32, 8, 96)
+
+
+def _expected_counts(w: synth.Workload, window=(-1, 0)):
+    nd = nc = npf = 0
+    G = w.n_q_heads // w.n_kv_heads
+    gw = min(G, 4)
+    rows_per_item = 64 * (4 // gw)
+    for n, L in zip(w.q_lens, w.k_lens):
+        if n == 1:
+            lo = 0 if window[0] < 0 else max(0, L - 1 - window[0])
+            splits = (L - 1) // 256 - lo // 256 + 1 if L > 0 else 1
+            nd += splits
+            nc += splits > 1
+        elif n > 1:
+            npf += math.ceil(n / rows_per_item) * (G // gw)
+    return nd, npf, nc
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
+def test_count_items_matches_closed_form(name):
+    w = getattr(synth, name)()
+    assert ops.count_items(w.q_lens, w.k_lens, 32, 8, (-1, 0)) == _expected_counts(w)
+
+
+def test_count_items_windows_and_groups():
+    w = synth.small_mixed(5, n_q_heads=8, n_kv_heads=8)
+    assert ops.count_items(w.q_lens, w.k_lens, 8, 8, (-1, 0)) == _expected_counts(w)
+    w = synth.small_mixed(6, n_q_heads=16, n_kv_heads=2)
+    assert ops.count_items(w.q_lens, w.k_lens, 16, 2, (300, 0)) == _expected_counts(w, (300, 0))
+    assert ops.count_items([1, 1], [0, 1], 32, 8, (-1, 0)) == (2, 0, 0)
+
+
+def test_copy_pages_rejects_bad_ids_on_the_host():
+    lib = _capi.lib()
+    ptrs = (ctypes.c_void_p * 1)(16)
+    src = (ctypes.c_int32 * 2)(0, 1)
+    dst = (ctypes.c_int32 * 2)(1, 2)
+    assert lib.hx_kv_copy_pages(ptrs, None, 1, src, dst, 2, 4, 1 << 19, None) == _capi.HX_E_OVERLAP
+    dst2 = (ctypes.c_int32 * 2)(3, 3)
+    assert lib.hx_kv_copy_pages(ptrs, None, 1, src, dst2, 2, 4, 1 << 19, None) == _capi.HX_E_OVERLAP
+    dst3 = (ctypes.c_int32 * 2)(2, 4)
+    assert lib.hx_kv_copy_pages(ptrs, None, 1, src, dst3, 2, 4, 1 << 19, None) == _capi.HX_E_INVALID_ARG
+    assert lib.hx_kv_copy_pages(ptrs, None, 1, src, dst, 0, 4, 1 << 19, None) == _capi.HX_OK
+
+
+def test_attention_entry_points_reject_bad_arguments_on_the_host():
+    lib = _capi.lib()
+    # workspace missing -> HX_E_WORKSPACE before any launch
+    assert lib.hx_varlen_attn_plan(16, 16, 16, 1, 1, 1, 1, 0, 256, 1, 32, 8, 128, -1, 0,
+                                   None, 0, None) == _capi.HX_E_WORKSPACE
+    # unsupported head_dim / group
+    assert lib.hx_varlen_attn_plan(16, 16, 16, 1, 1, 1, 1, 0, 256, 1, 32, 8, 64, -1, 0,
+                                   None, 0, None) == _capi.HX_E_UNSUPPORTED
+    # page size not a multiple of 256
+    assert lib.hx_varlen_attn_plan(16, 16, 16, 1, 1, 1, 1, 0, 128, 1, 32, 8, 128, -1, 0,
+                                   None, 0, None) == _capi.HX_E_INVALID_ARG
+    # append: bad element size
+    assert lib.hx_kv_append(16, 16, 10, 16, 8, 8, 16, 8, 8, 16, 1, 1, 8, 3, None) == _capi.HX_E_INVALID_ARG
+    # gather: length beyond the listed pages
+    assert lib.hx_kv_gather(16, 4, 256, 8, 128, 2, 16, 1, 257, 16, None) == _capi.HX_E_INVALID_ARG

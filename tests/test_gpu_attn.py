@@ -1,0 +1,175 @@
+"""Paged varlen GQA attention on the GPU against the float64 oracle.
+
+Tolerance (written in tests/gpu_cases.py): bf16/fp16 output within max-abs 2e-2 and
+mean-abs 2e-3 of the oracle evaluated on the same rounded inputs.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from helios_amd import ops, synth
+from tests.gpu_cases import DeviceTick, compare, host_append_reference, say
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+@pytest.mark.parametrize("exact_grid", [False, True])
+def test_c1_matches_golden_fixture(device, exact_grid):
+    say("c1 golden", exact_grid)
+    w = synth.c1(json.loads((GOLDEN / "c1_meta.json").read_text())["seed"])
+    tick = DeviceTick(w, torch.bfloat16, device)
+    out, lse = tick.attend(exact_grid=exact_grid, return_lse=True)
+    fixture = np.load(GOLDEN / "c1_bf16.npz")
+    compare(out, fixture["out"], what="c1 out")
+    assert np.abs(lse.cpu().numpy() - fixture["lse"]).max() < 5e-3
+    # host-side append of the same seeded inputs reproduces the device pool bits
+    xr = host_append_reference(w, torch.bfloat16)
+    for name in ("k_pool", "v_pool"):
+        dev = getattr(tick, name).float().cpu().numpy().astype(np.float64)
+        assert np.array_equal(dev, xr[name])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_small_mixed_ticks(device, dtype, seed):
+    say("mixed", seed, dtype)
+    w = synth.small_mixed(seed, batch=7, max_cached=1100, max_chunk=300, num_pages=64)
+    tick = DeviceTick(w, dtype, device)
+    ref, ref_lse = tick.oracle()
+    out, lse = tick.attend(exact_grid=seed % 2 == 0, return_lse=True)
+    compare(out, ref, what=f"mixed{seed} {dtype}")
+    assert np.abs(lse.cpu().numpy() - ref_lse).max() < 5e-3
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (64, 8), (4, 2), (32, 4)])
+def test_group_sizes(device, hq, hkv):
+    say("group", hq, hkv)
+    w = synth.small_mixed(10 + hq + hkv, n_q_heads=hq, n_kv_heads=hkv, batch=5, max_cached=700,
+                          max_chunk=400, num_pages=48)
+    tick = DeviceTick(w, torch.bfloat16, device)
+    ref, _ = tick.oracle()
+    compare(tick.attend(), ref, what=f"G={hq // hkv} hq={hq}")
+
+
+@pytest.mark.parametrize("window", [(-1, -1), (128, 0), (300, 2), (0, 0), (-1, 7), (1000, -1)])
+def test_windows(device, window):
+    say("window", window)
+    w = synth.small_mixed(30, batch=6, max_cached=900, max_chunk=260, num_pages=48)
+    tick = DeviceTick(w, torch.bfloat16, device)
+    ref, _ = tick.oracle(window=window)
+    compare(tick.attend(window=window, exact_grid=True), ref, what=f"window {window}")
+
+
+def test_c2_decode_tick(device):
+    say("c2 decode tick")
+    w = synth.c2()
+    tick = DeviceTick(w, torch.bfloat16, device, pool_on_device=True)
+    out = tick.attend(exact_grid=True)
+    ref, _ = tick.oracle()
+    compare(out, ref, what="c2")
+    out2 = tick.attend(exact_grid=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2), "grid sizing changed the result"
+
+
+def test_c3_mixed_tick(device):
+    say("c3 mixed tick")
+    w = synth.c3()
+    tick = DeviceTick(w, torch.bfloat16, device, pool_on_device=True)
+    out = tick.attend(exact_grid=True)
+    ref, _ = tick.oracle()
+    compare(out, ref, what="c3")
+
+
+def test_c4_long_context_shared_prefix(device):
+    say("c4 long context")
+    w = synth.c4()
+    tick = DeviceTick(w, torch.bfloat16, device, pool_on_device=True)
+    out = tick.attend(exact_grid=True)
+    chunk = 8
+    sample = list(range(0, 64)) + list(range(2016, 2080)) + list(range(4032, 4096))
+    ref, _ = tick.oracle(rows={b: [0] for b in range(8)} | {chunk: sample})
+    rows = np.array(list(range(8)) + [8 + r for r in sample])
+    compare(out, ref, what="c4 (decoders + 192 chunk rows)", rows=rows)
+
+
+def test_deterministic_across_runs(device):
+    say("determinism")
+    w = synth.small_mixed(44, batch=8, max_cached=3000, max_chunk=500, num_pages=96)
+    tick = DeviceTick(w, torch.bfloat16, device)
+    a = tick.attend()
+    b = tick.attend(exact_grid=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_packed_keys_without_block_table(device):
+    say("packed keys")
+    w = synth.small_mixed(50, batch=5, max_cached=600, max_chunk=200, num_pages=40)
+    tick = DeviceTick(w, torch.bfloat16, device)
+    ref, _ = tick.oracle()
+    # lay each sequence's keys out back to back, as non-paged varlen_attn takes them
+    keys = [torch.cat([tick.k_pool[p] for p in t])[:L] for t, L in zip(w.tables, w.k_lens)]
+    vals = [torch.cat([tick.v_pool[p] for p in t])[:L] for t, L in zip(w.tables, w.k_lens)]
+    k = torch.cat(keys).contiguous()
+    v = torch.cat(vals).contiguous()
+    out = ops.varlen_attn(tick.q, k, v, tick.cu_seq_q, tick.cu_seq_k, w.max_q, w.max_k,
+                          is_causal=True, enable_gqa=True)
+    compare(out, ref, what="packed keys")
+
+
+def test_rows_without_keys_are_zero(device):
+    say("empty rows")
+    H, D = 32, 128
+    pool = torch.randn(4, 256, 8, D, device=device).to(torch.bfloat16)
+    q = torch.randn(3, H, D, device=device).to(torch.bfloat16)
+    cu_q = torch.tensor([0, 1, 1, 3], dtype=torch.int32, device=device)   # seq 1 has no rows
+    used = torch.tensor([0, 5, 1], dtype=torch.int32, device=device)      # seq 2: 2 rows, 1 key
+    bt = torch.tensor([[0, 0], [1, 0], [2, 0]], dtype=torch.int32, device=device)
+    out, lse = ops.varlen_attn(q, pool, pool, cu_q, None, 2, 5, window_size=(-1, 0), enable_gqa=True,
+                               seqused_k=used, block_table=bt, return_aux=ops.AuxRequest(lse=True))
+    torch.cuda.synchronize()
+    assert not out[0].any() and torch.isinf(lse[:, 0]).all()     # decode row with L = 0
+    assert not out[1].any()                                       # row 0 of seq 2 sees key -1
+    ref = pool[2, 0].float().repeat_interleave(4, dim=0)
+    assert torch.allclose(out[2].float(), ref, atol=1e-2)        # row 1 sees only key 0
+
+
+def test_bad_page_id_is_reported_not_read(device):
+    say("bad page id")
+    w = synth.small_mixed(60, batch=3, max_cached=400, max_chunk=100, num_pages=16)
+    tick = DeviceTick(w, torch.bfloat16, device)
+    bt = tick.block_table.clone()
+    bt[0, 0] = 10_000
+    plan = ops.VarlenAttnPlan(tick.cu_seq_q, tick.cu_seq_k, tick.seqused_k, total_q=w.total_q,
+                              max_q=w.max_q, max_k=w.max_k, n_q_heads=32, n_kv_heads=8,
+                              head_dim=128, page_size=256, block_table_stride=bt.shape[1])
+    out = plan.run(tick.q, tick.k_pool, tick.v_pool, bt)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    assert plan.error_word() & 1
+
+
+def test_validation_errors(device):
+    say("validation")
+    w = synth.small_mixed(70, batch=2, num_pages=16)
+    tick = DeviceTick(w, torch.bfloat16, device)
+    with pytest.raises(ValueError):
+        ops.varlen_attn(tick.q, tick.k_pool, tick.v_pool, tick.cu_seq_q, tick.cu_seq_k, w.max_q,
+                        w.max_k, window_size=(-1, 0), enable_gqa=False, seqused_k=tick.seqused_k,
+                        block_table=tick.block_table)
+    with pytest.raises(ValueError):
+        ops.varlen_attn(tick.q.float(), tick.k_pool, tick.v_pool, tick.cu_seq_q, tick.cu_seq_k,
+                        w.max_q, w.max_k, enable_gqa=True, seqused_k=tick.seqused_k,
+                        block_table=tick.block_table)
+    with pytest.raises(ValueError):
+        ops.varlen_attn(tick.q, tick.k_pool, tick.v_pool, tick.cu_seq_q, tick.cu_seq_k, w.max_q,
+                        w.max_k, enable_gqa=True, seqused_k=tick.seqused_k,
+                        block_table=tick.block_table.long())
