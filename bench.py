@@ -1,0 +1,308 @@
+"""Benchmark of the paged-KV hot path on one MI355X.
+
+One step = one attention layer of a decode-only tick at Qwen3-4B shape: append the
+new token's K/V of 64 sequences into a 2048-page x 256-token pool (bf16, 8 KV heads,
+head_dim 128), then paged GQA decode attention of 32 query heads over context lengths
+uniform in [512, 4096] (seeded), page tables drawn from a shuffled free list.
+Synthetic N(0, 1) data. Steps rotate over four layer pools (2 GiB each) so no step
+finds the previous step's pages in cache.
+
+Printed JSON (one line):
+  value     algorithmic HBM bytes per step / step time, in GB/s: every visible key's K
+            and V row (8 heads x 128 x bf16, new token included), q read, o written,
+            and the append's read + write of the new rows.
+  roofline  the decode-attention kernel alone (HIP events around its launch inside the
+            timed loop): its algorithmic bytes (K/V + q + o) / its mean duration,
+            against the 8 TB/s HBM3E peak. `traffic` = HBM bytes per launch measured
+            by rocprofv3 FETCH_SIZE + WRITE_SIZE (scaled by a copy-kernel calibration)
+            when profiles/decode_c2_pmc.json holds that measurement, else null.
+  packed_tick  the mixed tick (32 decoders + 1024- and 992-token chunks): one layer's
+            append + attention time, and tokens/s of 36 such layers (attention and KV
+            work only; the model's GEMMs are not part of this path).
+  cpu_baseline  the reference's dense-KV path (gather, repeat_interleave, SDPA) in
+            torch fp32 on the host cores, on one full decode layer of the same tick.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+N_LAYERS_MODEL = 36
+POOL_COPIES = 4
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-packed-tick", action="store_true")
+    p.add_argument("--pmc-pass", action="store_true",
+                   help="short run for rocprofv3 counter collection: a calibration page "
+                        "copy of known size, then a few decode steps")
+    return p.parse_args()
+
+
+class DecodeBench:
+    """Device state of the decode tick: pools, new rows, metadata, plan."""
+
+    def __init__(self, w, device, copies: int):
+        import torch
+
+        from helios_amd import ops
+
+        self.w = w
+        self.device = device
+        shape = (w.num_pages, w.page_size, w.n_kv_heads, w.head_dim)
+        g = torch.Generator(device=device)
+        g.manual_seed(1234)
+        self.k_pools, self.v_pools = [], []
+        for _ in range(copies):
+            self.k_pools.append(torch.randn(shape, generator=g, device=device, dtype=torch.bfloat16))
+            self.v_pools.append(torch.randn(shape, generator=g, device=device, dtype=torch.bfloat16))
+        T = w.total_q
+        self.q = torch.randn((T, w.n_q_heads, w.head_dim), generator=g, device=device, dtype=torch.bfloat16)
+        self.k_new = torch.randn((T, w.n_kv_heads, w.head_dim), generator=g, device=device, dtype=torch.bfloat16)
+        self.v_new = torch.randn((T, w.n_kv_heads, w.head_dim), generator=g, device=device, dtype=torch.bfloat16)
+        self.slots = torch.from_numpy(w.write_slots()).to(device)
+        self.block_table = torch.from_numpy(w.block_table()).to(device)
+        cu_q = torch.tensor(w.cu_seq_q, dtype=torch.int32, device=device)
+        cu_k = torch.tensor(w.cu_seq_k, dtype=torch.int32, device=device)
+        used = torch.tensor(w.k_lens, dtype=torch.int32, device=device)
+        self.plan = ops.VarlenAttnPlan(
+            cu_q, cu_k, used, total_q=T, max_q=w.max_q, max_k=w.max_k,
+            n_q_heads=w.n_q_heads, n_kv_heads=w.n_kv_heads, head_dim=w.head_dim,
+            page_size=w.page_size, block_table_stride=self.block_table.shape[1],
+            window=(-1, 0), q_lens=w.q_lens, k_lens=w.k_lens)
+        self.out = torch.empty_like(self.q)
+        self.ops = ops
+
+    def step(self, layer: int, events=None):
+        kp, vp = self.k_pools[layer], self.v_pools[layer]
+        if events is not None:
+            events[0].record()
+        self.ops.kv_append(kp, vp, self.slots, self.k_new, self.v_new)
+        if events is not None:
+            events[1].record()
+        self.plan.run(self.q, kp, vp, self.block_table, out=self.out, phases=("decode",))
+        if events is not None:
+            events[2].record()
+        self.plan.run(self.q, kp, vp, self.block_table, out=self.out, phases=("combine", "chunk"))
+        if events is not None:
+            events[3].record()
+
+
+def cpu_baseline(w, seconds_budget: float = 20.0):
+    """The reference's dense-KV attention (oracle.dense_torch) on the host cores."""
+    import numpy as np
+    import torch
+
+    from oracle import dense_torch
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    used = sorted({p for t in w.tables for p in t})
+    remap = {p: i for i, p in enumerate(used)}
+    tables = [[remap[p] for p in t] for t in w.tables]
+    g = torch.Generator().manual_seed(5)
+    shape = (len(used), w.page_size, w.n_kv_heads, w.head_dim)
+    kp = torch.randn(shape, generator=g)
+    vp = torch.randn(shape, generator=g)
+    q = torch.randn((1, w.n_q_heads, w.total_q, w.head_dim), generator=g)
+    times = []
+    with torch.inference_mode():
+        for rep in range(2 + 5):
+            t0 = time.perf_counter()
+            dense_torch.packed_attention(q, kp, vp, tables, w.cached, w.q_lens)
+            dt = time.perf_counter() - t0
+            if rep >= 2:
+                times.append(dt)
+            if sum(times) > seconds_budget:
+                break
+    sec = statistics.median(times)
+    nbytes = w.decode_bytes()
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    del np
+    return {
+        "value": round(nbytes / sec / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"one full decode layer of the same tick ({w.batch} sequences, "
+                   f"{sum(w.k_lens)} keys), torch fp32 dense-KV path "
+                   f"(index_select gather, repeat_interleave, SDPA), median of {len(times)} "
+                   f"reps: {sec * 1e3:.1f} ms/layer; CPU: {cpu_model}"),
+    }
+
+
+def packed_tick(device, steps: int = 30, warmup: int = 5):
+    """One layer of the mixed tick: append + decode/chunk attention, wall time."""
+    import torch
+
+    from helios_amd import synth
+
+    w = synth.c3()
+    b = DecodeBench(w, device, copies=2)
+    for i in range(warmup):
+        b.step(i % 2)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        b.step(i % 2)
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    for i in range(steps):
+        b.step(i % 2, ev[i])
+    torch.cuda.synchronize()
+    decode_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in ev)
+    chunk_ms = statistics.mean(e[2].elapsed_time(e[3]) for e in ev)
+    res = {
+        "workload": "c3: 32 decoders ctx U[1024,4096] + chunks 1024@0 and 992@512, bf16",
+        "tokens": w.total_q,
+        "us_per_layer": round(sec * 1e6, 2),
+        "tick_ms_36_layers": round(sec * N_LAYERS_MODEL * 1e3, 3),
+        "tokens_per_s_attention_only": round(w.total_q / (sec * N_LAYERS_MODEL), 1),
+        "decode_rows_us": round(decode_ms * 1e3, 2),
+        "decode_rows_gbs": round(w.decode_bytes() / (decode_ms * 1e-3) / 1e9, 1),
+        "chunk_rows_us": round(chunk_ms * 1e3, 2),
+        "chunk_rows_tflops": round(w.chunk_flops() / (chunk_ms * 1e-3) / 1e12, 1),
+        "chunk_mfma_frac": round(w.chunk_flops() / (chunk_ms * 1e-3) / 2.5e15, 4),
+    }
+    del b
+    torch.cuda.empty_cache()
+    return res
+
+
+def pmc_pass(device):
+    """Counter-collection run: a page copy of known size, then decode steps."""
+    import torch
+
+    from helios_amd import ops, synth
+
+    layers = 4
+    pools = [torch.zeros((256, 256, 8, 128), dtype=torch.bfloat16, device=device) for _ in range(layers)]
+    src, dst = list(range(0, 64)), list(range(128, 192))
+    for _ in range(3):
+        ops.kv_copy_pages(pools, None, src, dst)
+    torch.cuda.synchronize()
+    copy_bytes = layers * 64 * pools[0][0].numel() * 2
+    b = DecodeBench(synth.c2(), device, copies=POOL_COPIES)
+    for i in range(8):
+        b.step(i % POOL_COPIES)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_pass": True, "copy_read_bytes_per_dispatch": copy_bytes,
+                      "copy_write_bytes_per_dispatch": copy_bytes,
+                      "decode_algorithmic_bytes": b.w.decode_bytes()}), flush=True)
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the paged-KV "
+              "path has no multi-GPU form in this build.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from helios_amd import _capi, synth
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm device", file=sys.stderr)
+        sys.exit(1)
+    _capi.lib()
+    device = torch.device("cuda", 0)
+    if args.pmc_pass:
+        pmc_pass(device)
+        return
+
+    w = synth.c2()
+    b = DecodeBench(w, device, copies=POOL_COPIES)
+    step_bytes = w.decode_bytes() + w.append_bytes()
+    for i in range(args.warmup):
+        b.step(i % POOL_COPIES)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        b.step(i % POOL_COPIES, events[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    assert b.plan.error_word() == 0, "attention plan reported an error"
+    ms_per_step = elapsed * 1e3 / args.steps
+    append_us = statistics.mean(e[0].elapsed_time(e[1]) for e in events) * 1e3
+    decode_us = statistics.mean(e[1].elapsed_time(e[2]) for e in events) * 1e3
+    combine_us = statistics.mean(e[2].elapsed_time(e[3]) for e in events) * 1e3
+    kernel_bytes = w.decode_bytes()
+    achieved = kernel_bytes / (decode_us * 1e-6) / 1e9
+    traffic = None
+    pmc = ROOT / "profiles" / "decode_c2_pmc.json"
+    if pmc.exists():
+        try:
+            traffic = json.loads(pmc.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    result = {
+        "metric": "paged decode attn HBM GB/s (% peak) + packed-tick tokens/s, Qwen3-4B shape",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) K/V/q, seeded context lengths and page tables",
+        "config": {
+            "workload": "decode-only tick, one attention layer incl. KV append: 64 seqs, ctx "
+                        "U[512,4096] seeded, 32q/8kv heads, d=128, 2048-page x 256-token pool",
+            "batch": w.batch,
+            "keys": sum(w.k_lens),
+            "step_bytes": step_bytes,
+            "pct_peak": round(100 * value / HBM_PEAK_GBS, 2),
+            "ms_per_tick_36_layers": round(ms_per_step * N_LAYERS_MODEL, 4),
+            "kernel_us": {"kv_append": round(append_us, 2), "decode_attention": round(decode_us, 2),
+                          "split_combine": round(combine_us, 2)},
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode_kernel (paged split-K decode attention)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": kernel_bytes,
+        },
+    }
+    del b, events
+    torch.cuda.empty_cache()
+    if not args.no_packed_tick:
+        result["packed_tick"] = packed_tick(device)
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(w)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -30,6 +30,11 @@ struct Elem<__bf16> {
     __bf16 h = (__bf16)f;  // round to nearest even
     return __builtin_bit_cast(uint16_t, h);
   }
+  // c + a.lo*b.lo + a.hi*b.hi for two packed pairs (v_dot2_f32_bf16).
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+  }
 };
 
 template <>
@@ -37,6 +42,10 @@ struct Elem<_Float16> {
   typedef f16x8_t v8;
   static __device__ __forceinline__ f32x4_t mfma16x16x32(v8 a, v8 b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
   }
   static __device__ __forceinline__ float lo(uint32_t w) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
@@ -56,6 +65,36 @@ __device__ __forceinline__ typename Elem<T>::v8 as_v8(uint4 u) {
 }
 
 __device__ __forceinline__ uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
+
+// 16-byte load with the non-temporal hint: K/V rows are streamed once per tick, and
+// streaming them past the caches leaves L2 to the split partials and metadata.
+__device__ __forceinline__ uint4 ld16_stream(const void* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// 8 packed elements . 8 packed elements + c, in fp32 (four dot2 steps).
+template <typename T>
+__device__ __forceinline__ float dot8(uint4 a, uint4 b, float c) {
+  c = Elem<T>::dot2(a.x, b.x, c);
+  c = Elem<T>::dot2(a.y, b.y, c);
+  c = Elem<T>::dot2(a.z, b.z, c);
+  return Elem<T>::dot2(a.w, b.w, c);
+}
+
+// Cross-lane moves within a 16-lane row (DPP). Each pairing is an involution:
+// xor1 / xor2 within quads, half-mirror (lane ^ 7 within 8), mirror (lane ^ 15).
+enum : int {
+  kDppXor1 = 0xB1,        // quad_perm [1,0,3,2]
+  kDppXor2 = 0x4E,        // quad_perm [2,3,0,1]
+  kDppHalfMirror = 0x141, // row_half_mirror
+  kDppMirror = 0x140,     // row_mirror
+};
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
 
 __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
   return (uint32_t)lo | ((uint32_t)hi << 16);

@@ -11,9 +11,10 @@
 //                   work lists into the workspace. Run once per tick, reused per layer.
 //   decode_kernel   one workgroup per (256-key split, KV head). The G query heads of the
 //                   KV group share one read of the split's K and V (64 KiB each at
-//                   Qwen3-4B shape). QK^T runs on a 16x16x32 MFMA with the G heads as
-//                   rows; softmax uses wavefront xor-reductions plus a 4-wave LDS step;
-//                   PV runs on VALU with each 16-lane group streaming whole 256-byte V rows.
+//                   Qwen3-4B shape), streamed as whole 256-byte rows per 16-lane group.
+//                   QK^T runs on VALU dot2 with a DPP reduce-scatter across the 16 lanes;
+//                   softmax uses DPP wave reductions plus a 4-wave LDS step; PV runs on
+//                   VALU in fp32.
 //                   A sequence that fits one split writes its output directly; longer ones
 //                   write fp32 partials (m, l, o).
 //   combine_kernel  merges the partials of each long decode sequence in split order, so
@@ -217,9 +218,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
     if (active) {
       a.seq_info[b] = make_int4(q0, n, L, kvb);
       for (int k = 0; k < nd; ++k) {
-        if (off_d + k < a.max_dec) a.dec_items[off_d + k] = make_int4(b, s_first + k, splits, off_d);
+        if (off_d + k < a.max_dec) a.dec_items[off_d + k] = make_int4(b, s_first + k, q0, L);
       }
-      if (nc) a.comb_seqs[off_c] = make_int4(b, off_d, splits, 0);
+      if (nc) a.comb_seqs[off_c] = make_int4(b, off_d, splits, q0);
       // Later row blocks see more keys under a causal mask: list them first.
       int k = 0;
       for (int blk = nblk - 1; blk >= 0; --blk) {
@@ -279,12 +280,22 @@ struct RunArgs {
 // True when the workspace holds a plan for this run's shape; otherwise the block
 // raises HX_WERR_PLAN_MISMATCH (once) and the caller must return without touching
 // the work lists.
-__device__ __forceinline__ bool plan_matches(const RunArgs& a) {
-  const int32_t* h = a.hdr;
-  const bool ok = h[H_STAMP] == kPlanStamp && h[H_BATCH] == a.batch && h[H_MAXQ] == a.max_q &&
-                  h[H_MAXK] == a.max_k && h[H_HQ] == a.hq && h[H_HKV] == a.hkv;
-  if (!ok && blockIdx.x == 0 && threadIdx.x == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_PLAN_MISMATCH);
-  return ok;
+// The header is read with three wide loads issued together and compared with
+// non-short-circuit ands, so the check costs one memory round trip.
+struct Header {
+  int4 counts;  // H_NDEC, H_NPF, H_NCOMB, H_ERR
+  bool ok;
+};
+__device__ __forceinline__ Header read_header(const RunArgs& a) {
+  const int4 h0 = *reinterpret_cast<const int4*>(a.hdr);
+  const int4 h1 = *reinterpret_cast<const int4*>(a.hdr + 4);
+  const int2 h2 = *reinterpret_cast<const int2*>(a.hdr + 8);
+  Header r;
+  r.counts = h0;
+  r.ok = (h2.y == kPlanStamp) & (h1.x == a.batch) & (h1.y == a.max_q) & (h1.z == a.max_k) &
+         (h1.w == a.hq) & (h2.x == a.hkv);
+  if (!r.ok && blockIdx.x == 0 && threadIdx.x == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_PLAN_MISMATCH);
+  return r;
 }
 
 template <typename T>
@@ -293,30 +304,92 @@ __device__ __forceinline__ uint4 ld16(const T* p) {
 }
 
 // ------------------------------------------------------------------ decode (split-K)
+// Reduce-scatter across the 16 lanes of a row group: lane c holds partial dot products
+// part[i][h] of rows i = 0..15 over its own 8 dims; afterwards out[h] is the full dot
+// product of row c. Four DPP butterfly steps (mirror, half-mirror, xor 2, xor 1), each
+// pairing lanes that differ in one more bit of c and agree on the bits already used.
+template <int G>
+__device__ __forceinline__ void row_reduce_scatter(float (&part)[16][G], float (&out)[G], int c) {
+  const bool b3 = c & 8, b2 = c & 4, b1 = c & 2, b0 = c & 1;
+  float s8[8][G], s4[4][G], s2[2][G];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float lo = part[j][h] + hx::dpp<hx::kDppMirror>(part[j][h]);
+      const float hi = part[j + 8][h] + hx::dpp<hx::kDppMirror>(part[j + 8][h]);
+      s8[j][h] = b3 ? hi : lo;
+    }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float lo = s8[j][h] + hx::dpp<hx::kDppHalfMirror>(s8[j][h]);
+      const float hi = s8[j + 4][h] + hx::dpp<hx::kDppHalfMirror>(s8[j + 4][h]);
+      s4[j][h] = b2 ? hi : lo;
+    }
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float lo = s4[j][h] + hx::dpp<hx::kDppXor2>(s4[j][h]);
+      const float hi = s4[j + 2][h] + hx::dpp<hx::kDppXor2>(s4[j + 2][h]);
+      s2[j][h] = b1 ? hi : lo;
+    }
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float lo = s2[0][h] + hx::dpp<hx::kDppXor1>(s2[0][h]);
+    const float hi = s2[1][h] + hx::dpp<hx::kDppXor1>(s2[1][h]);
+    out[h] = b0 ? hi : lo;
+  }
+}
+
+// Max / sum over all 64 lanes: DPP inside each 16-lane row, then across rows.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, hx::dpp<hx::kDppXor1>(v));
+  v = fmaxf(v, hx::dpp<hx::kDppXor2>(v));
+  v = fmaxf(v, hx::dpp<hx::kDppHalfMirror>(v));
+  v = fmaxf(v, hx::dpp<hx::kDppMirror>(v));
+  v = fmaxf(v, __shfl_xor(v, 16));
+  return fmaxf(v, __shfl_xor(v, 32));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += hx::dpp<hx::kDppXor1>(v);
+  v += hx::dpp<hx::kDppXor2>(v);
+  v += hx::dpp<hx::kDppHalfMirror>(v);
+  v += hx::dpp<hx::kDppMirror>(v);
+  v += __shfl_xor(v, 16);
+  return v + __shfl_xor(v, 32);
+}
+
 template <typename T, int G>
 __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
   typedef hx::Elem<T> E;
   constexpr int GP = G <= 4 ? 4 : 8;      // floats per token in p_lds
-  constexpr int NHG = (G + 3) / 4;        // 16-lane groups holding valid heads in the MFMA output
   __shared__ __attribute__((aligned(16))) float p_lds[kSplit * GP];
-  __shared__ float red_max[4][16];
-  __shared__ float red_sum[4][16];
-  __shared__ float red_o[G * 8][kThreads];
-  __shared__ float fin_m[16];
-  __shared__ float fin_l[16];
+  __shared__ float red_max[4][8];
+  __shared__ float red_sum[4][8];
+  // Row stride kThreads + 8 floats: the 64 lanes of a wave reading (e, c) pairs of the
+  // final sum hit 64 distinct banks.
+  __shared__ float red_o[G * 8][kThreads + 8];
+  __shared__ float fin_m[8];
+  __shared__ float fin_l[8];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int item = (int)blockIdx.x / a.hkv;
   const int g = (int)blockIdx.x - item * a.hkv;
-  if (!plan_matches(a)) return;
-  const int n_dec = a.hdr[H_NDEC];
+  // The work item is read together with the header (item < grid_dec <= the list's
+  // capacity, so the read stays inside the workspace) and used only once both check out.
+  const Header hd = read_header(a);
+  const int4 it = a.dec_items[item];  // {b, split, q0, L}
+  if (!hd.ok) return;
+  const int n_dec = hd.counts.x;
   if (blockIdx.x == 0 && tid == 0 && n_dec > a.grid_dec) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
   if (item >= n_dec) return;
-  const int4 it = a.dec_items[item];
-  const int b = it.x, s = it.y, splits = it.z;
+  const int b = it.x, s = it.y, q0 = it.z, L = it.w;
   if ((unsigned)b >= (unsigned)a.batch) return;
-  const int4 si = a.seq_info[b];
-  const int q0 = si.x, L = si.z;
+  int s_first, splits;
+  decode_splits(L, a.win_left, &s_first, &splits);
   const int key0 = s * kSplit;
   const int kb = max(decode_lo(L, a.win_left), key0);
   const int ke = min(L, key0 + kSplit);
@@ -329,113 +402,102 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
     if (!page_ok && tid == 0 && kb < ke) atomicOr(&a.hdr[H_ERR], HX_WERR_BAD_PAGE);
     row0 = (int64_t)(page_ok ? page : 0) * a.page_size + key0 % a.page_size;
   } else {
-    row0 = (int64_t)si.w + key0;
+    row0 = (int64_t)a.seq_info[b].w + key0;
   }
   const int kvr = (int)a.kv_row;
   const T* kbase = reinterpret_cast<const T*>(a.k) + row0 * a.kv_row + (int64_t)g * a.kv_head;
   const T* vbase = reinterpret_cast<const T*>(a.v) + row0 * a.kv_row + (int64_t)g * a.kv_head;
 
-  // K as the MFMA B operand: lane holds token 64w+16tb+(lane&15), dims 32st+8(lane>>4)..+7.
-  uint4 kf[4][4];
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    const int n = 64 * w + 16 * tb + (lane & 15);
-    const bool ok = page_ok && key0 + n >= kb && key0 + n < ke;
-    const T* rp = kbase + n * kvr + 8 * (lane >> 4);
-#pragma unroll
-    for (int st = 0; st < 4; ++st) kf[tb][st] = ok ? ld16(rp + 32 * st) : hx::zero4();
-  }
-  // V rows for the VALU PV: a 16-lane group covers one 256-byte row.
-  uint4 vr[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int n = 64 * w + 4 * i + (lane >> 4);
-    const bool ok = page_ok && key0 + n >= kb && key0 + n < ke;
-    vr[i] = ok ? ld16(vbase + n * kvr + 8 * (lane & 15)) : hx::zero4();
-  }
-  // q as the MFMA A operand: row = head (lane&15) of the group, zero rows beyond G.
-  uint4 qf[4];
+  // Lane (r, c) = (lane / 16, lane % 16) owns the 16-byte chunk c (dims 8c..8c+7) of
+  // tokens 64w + 4i + r, i = 0..15: every wave instruction reads four whole 256-byte
+  // head rows, the access pattern that streams at full HBM rate (16 rows x 64 B per
+  // instruction, the MFMA fragment layout, does not).
+  const int r = lane >> 4, c = lane & 15;
+  uint4 qf[G];
   {
-    const int m = lane & 15;
-    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)q0 * a.q_row +
-                  (int64_t)(g * G + (m < G ? m : 0)) * a.q_head + 8 * (lane >> 4);
+    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)q0 * a.q_row + (int64_t)(g * G) * a.q_head + 8 * c;
 #pragma unroll
-    for (int st = 0; st < 4; ++st) qf[st] = m < G ? ld16(qp + 32 * st) : hx::zero4();
+    for (int h = 0; h < G; ++h) qf[h] = ld16(qp + (int64_t)h * a.q_head);
   }
-
-  // S = q K^T: lane holds heads 4(lane>>4)+i for token 16tb+(lane&15).
-  hx::f32x4_t sacc[4];
+  // Rows outside [kb, ke) re-read the split's first visible row (same cache lines,
+  // always inside the buffer): that data is finite, its score is masked to -inf below
+  // and its p is 0, so it needs no zeroing and all 32 loads issue back to back under one
+  // uniform branch. An empty split (no visible key, or a bad page id) loads nothing and
+  // uses zero registers.
+  uint4 kr[16], vr[16];
+  const bool any = page_ok && kb < ke;
+  const int nfirst = kb - key0;
+  const int nend = ke - key0;
+  if (any) {
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    sacc[tb] = hx::f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 16; ++i) {
+      const int n = 64 * w + 4 * i + r;
+      kr[i] = hx::ld16_stream(kbase + ((n >= nfirst && n < nend) ? n : nfirst) * kvr + 8 * c);
+    }
 #pragma unroll
-    for (int st = 0; st < 4; ++st)
-      sacc[tb] = E::mfma16x16x32(hx::as_v8<T>(qf[st]), hx::as_v8<T>(kf[tb][st]), sacc[tb]);
-  }
-
-  const int hg = lane >> 4;
-  float sc[4][4];
-  float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    for (int i = 0; i < 16; ++i) {
+      const int n = 64 * w + 4 * i + r;
+      vr[i] = hx::ld16_stream(vbase + ((n >= nfirst && n < nend) ? n : nfirst) * kvr + 8 * c);
+    }
+  } else {
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    const int key = key0 + 64 * w + 16 * tb + (lane & 15);
-    const bool ok = page_ok && key >= kb && key < ke;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sc[tb][i] = ok ? sacc[tb][i] * a.scale_log2 : -INFINITY;
-      mx[i] = fmaxf(mx[i], sc[tb][i]);
+    for (int i = 0; i < 16; ++i) {
+      kr[i] = hx::zero4();
+      vr[i] = hx::zero4();
     }
   }
+
+  // q . k on VALU (packed dot2, fp32 accumulate), then the 16 lanes of each row group
+  // exchange partial sums so that lane (r, c) ends with token 64w + 4c + r.
+  float part[16][G];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) mx[i] = hx::wave_max_xor(mx[i], 1, 8);
-  if ((lane & 15) == 0 && hg < NHG) {
+  for (int i = 0; i < 16; ++i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red_max[w][4 * hg + i] = mx[i];
+    for (int h = 0; h < G; ++h) part[i][h] = hx::dot8<T>(qf[h], kr[i], 0.f);
+  float sc[G];
+  row_reduce_scatter<G>(part, sc, c);
+
+  const int t = 64 * w + 4 * c + r;
+  const bool tok_ok = page_ok && key0 + t >= kb && key0 + t < ke;
+  float mx[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    sc[h] = tok_ok ? sc[h] * a.scale_log2 : -INFINITY;
+    mx[h] = wave_max(sc[h]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) red_max[w][h] = mx[h];
   }
   __syncthreads();
-  float m[4];
+  float ps[G];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m[i] = -INFINITY;
-    if (hg < NHG) {
-#pragma unroll
-      for (int ww = 0; ww < 4; ++ww) m[i] = fmaxf(m[i], red_max[ww][4 * hg + i]);
-    }
+  for (int h = 0; h < G; ++h) {
+    const float m = fmaxf(fmaxf(red_max[0][h], red_max[1][h]), fmaxf(red_max[2][h], red_max[3][h]));
+    const float p = sc[h] == -INFINITY ? 0.f : exp2f(sc[h] - m);
+    sc[h] = p;
+    ps[h] = wave_sum(p);
   }
-  float ps[4] = {0.f, 0.f, 0.f, 0.f};
+  if (lane == 0) {
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float p = sc[tb][i] == -INFINITY ? 0.f : exp2f(sc[tb][i] - m[i]);
-      sc[tb][i] = p;
-      ps[i] += p;
-    }
+    for (int h = 0; h < G; ++h) red_sum[w][h] = ps[h];
   }
+  if (G >= 4) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) ps[i] = hx::wave_sum_xor(ps[i], 1, 8);
-  if ((lane & 15) == 0 && hg < NHG) {
+    for (int h = 0; h < G; h += 4)
+      *reinterpret_cast<float4*>(&p_lds[t * GP + h]) = make_float4(sc[h], sc[h + 1], sc[h + 2], sc[h + 3]);
+  } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red_sum[w][4 * hg + i] = ps[i];
-  }
-  if (hg < NHG) {
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      const int n = 64 * w + 16 * tb + (lane & 15);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (4 * hg + i < G) p_lds[n * GP + 4 * hg + i] = sc[tb][i];
-    }
+    for (int h = 0; h < G; ++h) p_lds[t * GP + h] = sc[h];
   }
   __syncthreads();
 
-  // O = P V on VALU, fp32 accumulate.
+  // O = P V on VALU, fp32 accumulate: row 64w+4i+r of V meets p of the same token.
   float o[G][8];
 #pragma unroll
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
-  const int r = lane >> 4;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int n = 64 * w + 4 * i + r;
@@ -473,12 +535,12 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
   __syncthreads();
 
   for (int oi = tid; oi < G * kD; oi += kThreads) {
-    const int h = oi >> 7, d = oi & (kD - 1), c = d >> 3, e = d & 7;
+    const int h = oi >> 7, d = oi & (kD - 1), cc = d >> 3, e = d & 7;
     float acc = 0.f;
 #pragma unroll
     for (int ww = 0; ww < 4; ++ww)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) acc += red_o[h * 8 + e][ww * 64 + rr * 16 + c];
+      for (int rr = 0; rr < 4; ++rr) acc += red_o[h * 8 + e][ww * 64 + rr * 16 + cc];
     const float mh = fin_m[h], lh = fin_l[h];
     const int qh = g * G + h;
     if (splits == 1) {
@@ -494,36 +556,62 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
 }
 
 // ------------------------------------------------------------------ split combine
+// One thread per (head, dim) output: the partial rows of a sequence are merged with an
+// online max in chunks of 16 splits, each chunk's 16 (m, l) pairs and 16 partial values
+// loaded together, so a sequence of up to 16 splits costs one memory round trip.
 template <typename T, int G>
 __global__ __launch_bounds__(kThreads) void combine_kernel(RunArgs a) {
   typedef hx::Elem<T> E;
+  constexpr int kChunk = 16;
   const int cs = (int)blockIdx.x / a.hkv;
   const int g = (int)blockIdx.x - cs * a.hkv;
-  if (!plan_matches(a)) return;
-  const int n_comb = a.hdr[H_NCOMB];
+  const Header hd = read_header(a);
+  const int4 c = a.comb_seqs[cs];  // {b, first item, splits, q0}; cs < grid_comb <= batch
+  if (!hd.ok) return;
+  const int n_comb = hd.counts.z;
   if (blockIdx.x == 0 && threadIdx.x == 0 && n_comb > a.grid_comb) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
   if (cs >= n_comb) return;
-  const int4 c = a.comb_seqs[cs];
-  const int first = c.y, splits = c.z;
+  const int first = c.y, splits = c.z, q0 = c.w;
   if ((unsigned)c.x >= (unsigned)a.batch || first < 0 || splits < 1) return;
-  if ((int64_t)first + splits > (int64_t)a.hdr[H_NDEC]) return;
-  const int q0 = a.seq_info[c.x].x;
+  if ((int64_t)first + splits > (int64_t)hd.counts.x) return;
   for (int oi = threadIdx.x; oi < G * kD; oi += kThreads) {
     const int h = oi >> 7, d = oi & (kD - 1);
     const int qh = g * G + h;
-    float M = -INFINITY;
-    for (int s = 0; s < splits; ++s) M = fmaxf(M, a.part_ml[(int64_t)(first + s) * a.hq + qh].x);
-    float lsum = 0.f, acc = 0.f;
-    for (int s = 0; s < splits; ++s) {
-      const float2 ml = a.part_ml[(int64_t)(first + s) * a.hq + qh];
-      const float wgt = ml.x == -INFINITY ? 0.f : exp2f(ml.x - M);
-      lsum += wgt * ml.y;
-      acc += wgt * a.part_o[((int64_t)(first + s) * a.hq + qh) * kD + d];
+    const float2* ml = a.part_ml + (int64_t)first * a.hq + qh;
+    const float* po = a.part_o + ((int64_t)first * a.hq + qh) * kD + d;
+    const int64_t step_o = (int64_t)a.hq * kD;
+    float m_run = -INFINITY, l_run = 0.f, acc = 0.f;
+    for (int s0 = 0; s0 < splits; s0 += kChunk) {
+      float2 mlv[kChunk];
+      float ov[kChunk];
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j) {
+        const int sj = s0 + j < splits ? s0 + j : splits - 1;  // clamp: duplicates get weight 0
+        mlv[j] = ml[(int64_t)sj * a.hq];
+        ov[j] = po[(int64_t)sj * step_o];
+      }
+      float cm = m_run;
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j)
+        if (s0 + j < splits) cm = fmaxf(cm, mlv[j].x);
+      if (cm != -INFINITY) {
+        const float rescale = m_run == -INFINITY ? 0.f : exp2f(m_run - cm);
+        l_run *= rescale;
+        acc *= rescale;
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+          const bool live = s0 + j < splits && mlv[j].x != -INFINITY;
+          const float wgt = live ? exp2f(mlv[j].x - cm) : 0.f;
+          l_run += wgt * mlv[j].y;
+          acc += wgt * ov[j];
+        }
+        m_run = cm;
+      }
     }
-    const float val = lsum > 0.f ? acc / lsum : 0.f;
+    const float val = l_run > 0.f ? acc / l_run : 0.f;
     reinterpret_cast<uint16_t*>(a.out)[(int64_t)q0 * a.o_row + (int64_t)qh * a.o_head + d] = E::bits(val);
     if (a.lse && d == 0)
-      a.lse[(int64_t)qh * a.total_q + q0] = lsum > 0.f ? (M + log2f(lsum)) * kLn2 : -INFINITY;
+      a.lse[(int64_t)qh * a.total_q + q0] = l_run > 0.f ? (m_run + log2f(l_run)) * kLn2 : -INFINITY;
   }
 }
 
@@ -543,11 +631,12 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(RunArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int item = (int)blockIdx.x / a.hkv;
   const int g = (int)blockIdx.x - item * a.hkv;
-  if (!plan_matches(a)) return;
-  const int n_pf = a.hdr[H_NPF];
+  const Header hd = read_header(a);
+  const int4 it = a.pf_items[item];  // item < grid_pf <= the list's capacity
+  if (!hd.ok) return;
+  const int n_pf = hd.counts.y;
   if (blockIdx.x == 0 && tid == 0 && n_pf > a.grid_pf) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
   if (item >= n_pf) return;
-  const int4 it = a.pf_items[item];
   const int b = it.x, row0 = it.y, hquad = it.z;
   if ((unsigned)b >= (unsigned)a.batch) return;
   const int4 si = a.seq_info[b];

@@ -293,8 +293,15 @@ class VarlenAttnPlan:
         scale: float | None = None,
         out: torch.Tensor | None = None,
         return_lse: bool = False,
+        phases: tuple[str, ...] = ("decode", "combine", "chunk"),
     ) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
+        """Attention for one layer. ``phases`` launches a subset of the three kernels
+        (decode splits, split combine, chunk rows); a full result needs all three, in
+        that order, into the same ``out``. Profilers use it to time each kernel."""
         _require_gpu(query, k_cache, v_cache)
+        unknown = set(phases) - {"decode", "combine", "chunk"}
+        if unknown:
+            raise ValueError(f"unknown attention phases {sorted(unknown)}")
         if query.device != self.device:
             raise ValueError("Query is not on the plan's device.")
         if query.dtype not in _SUPPORTED:
@@ -346,7 +353,9 @@ class VarlenAttnPlan:
             scale, self.window[0], self.window[1], _SUPPORTED[query.dtype],
             out.data_ptr(), out.stride(0), out.stride(1),
             None if lse is None else lse.data_ptr(),
-            self.hints[0], self.hints[1], self.hints[2],
+            self.hints[0] if "decode" in phases else 0,
+            self.hints[1] if "chunk" in phases else 0,
+            self.hints[2] if "combine" in phases else 0,
             self.ws_ptr, self.ws_bytes, _stream_ptr(query.device),
         )
         _capi.check(code, "hx_varlen_attn_run")

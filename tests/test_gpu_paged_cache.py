@@ -121,6 +121,6 @@ def test_restore_by_copy_gives_private_identical_pages(device):
         outs.append(b.attend(0, q, k, v))
         b.advance(1)
     assert torch.equal(outs[0], outs[1])
-    del snap, src, shared, private, batch, b
+    del snap, src, shared, private, batch, b, cache
     gc.collect()
     assert pool.free_pages == pool.num_pages
