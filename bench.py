@@ -11,9 +11,11 @@ Printed JSON (one line):
   value     algorithmic HBM bytes per step / step time, in GB/s: every visible key's K
             and V row (8 heads x 128 x bf16, new token included), q read, o written,
             and the append's read + write of the new rows.
-  roofline  the decode-attention kernel alone (HIP events around its launch inside the
-            timed loop): its algorithmic bytes (K/V + q + o) / its mean duration,
-            against the 8 TB/s HBM3E peak. `traffic` = HBM bytes per launch measured
+  roofline  the decode-attention kernel alone (HIP events around its launch, in a second
+            pass over the same steps so that the timed loop carries no event markers;
+            the kernel also performs the tick's KV append): its algorithmic bytes
+            (K/V + q + o + the append's read and write) / its mean duration, against
+            the 8 TB/s HBM3E peak. `traffic` = HBM bytes per launch measured
             by rocprofv3 FETCH_SIZE + WRITE_SIZE (scaled by a copy-kernel calibration)
             when profiles/decode_c2_pmc.json holds that measurement, else null.
   packed_tick  the mixed tick (32 decoders + 1024- and 992-token chunks): one layer's
@@ -89,13 +91,19 @@ class DecodeBench:
         self.ops = ops
 
     def step(self, layer: int, events=None):
+        """Append the new rows and attend, as PagedBatchCache.attend does. Decode-only
+        ticks append inside the decode kernel; ticks with chunk rows append first.
+        events[0..3] bracket (append, decode, combine + chunk)."""
         kp, vp = self.k_pools[layer], self.v_pools[layer]
+        fused = self.w.max_q == 1
         if events is not None:
             events[0].record()
-        self.ops.kv_append(kp, vp, self.slots, self.k_new, self.v_new)
+        if not fused:
+            self.ops.kv_append(kp, vp, self.slots, self.k_new, self.v_new)
         if events is not None:
             events[1].record()
-        self.plan.run(self.q, kp, vp, self.block_table, out=self.out, phases=("decode",))
+        self.plan.run(self.q, kp, vp, self.block_table, out=self.out, phases=("decode",),
+                      append=(self.k_new, self.v_new, self.slots) if fused else None)
         if events is not None:
             events[2].record()
         self.plan.run(self.q, kp, vp, self.block_table, out=self.out, phases=("combine", "chunk"))
@@ -238,19 +246,25 @@ def main():
     step_bytes = w.decode_bytes() + w.append_bytes()
     for i in range(args.warmup):
         b.step(i % POOL_COPIES)
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    # Timed region: K steps, wall clock, synchronised on both sides (no events inside).
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        b.step(i % POOL_COPIES, events[i])
+        b.step(i % POOL_COPIES)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     assert b.plan.error_word() == 0, "attention plan reported an error"
     ms_per_step = elapsed * 1e3 / args.steps
+    # Kernel timing: the same K steps again with HIP events around each launch, on the
+    # stream the kernels run on (the current stream).
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        b.step(i % POOL_COPIES, events[i])
+    torch.cuda.synchronize()
     append_us = statistics.mean(e[0].elapsed_time(e[1]) for e in events) * 1e3
     decode_us = statistics.mean(e[1].elapsed_time(e[2]) for e in events) * 1e3
     combine_us = statistics.mean(e[2].elapsed_time(e[3]) for e in events) * 1e3
-    kernel_bytes = w.decode_bytes()
+    kernel_bytes = w.decode_bytes() + w.append_bytes()  # the decode kernel appends too
     achieved = kernel_bytes / (decode_us * 1e-6) / 1e9
     traffic = None
     pmc = ROOT / "profiles" / "decode_c2_pmc.json"
@@ -281,12 +295,13 @@ def main():
             "step_bytes": step_bytes,
             "pct_peak": round(100 * value / HBM_PEAK_GBS, 2),
             "ms_per_tick_36_layers": round(ms_per_step * N_LAYERS_MODEL, 4),
-            "kernel_us": {"kv_append": round(append_us, 2), "decode_attention": round(decode_us, 2),
+            "kernel_us": {"kv_append_separate": round(append_us, 2),
+                          "decode_attention_with_append": round(decode_us, 2),
                           "split_combine": round(combine_us, 2)},
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_kernel (paged split-K decode attention)",
+            "kernel": "decode_kernel (paged split-K decode attention with the fused KV append)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

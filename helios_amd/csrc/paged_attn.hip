@@ -16,7 +16,9 @@
 //                   softmax uses DPP wave reductions plus a 4-wave LDS step; PV runs on
 //                   VALU in fp32.
 //                   A sequence that fits one split writes its output directly; longer ones
-//                   write fp32 partials (m, l, o).
+//                   write partials: fp32 (m, l) and o / l rounded to bf16 (the partial
+//                   stores cost more than their 1.6% of the bytes suggests, so they are
+//                   halved; the extra error is one more bf16 rounding of the output).
 //   combine_kernel  merges the partials of each long decode sequence in split order, so
 //                   results do not depend on scheduling.
 //   chunk_kernel    prefill chunks: 4 waves per workgroup, each wave owning 64 query rows
@@ -81,7 +83,7 @@ inline Layout make_layout(int batch, int max_q, int max_k, int hq, int hkv) {
   l.comb_seqs = off; off = align256(off + (size_t)batch * sizeof(int4));
   l.pf_items = off;  off = align256(off + (size_t)l.max_pf * sizeof(int4));
   l.part_ml = off;   off = align256(off + (size_t)l.max_dec * hq * sizeof(float2));
-  l.part_o = off;    off = align256(off + (size_t)l.max_dec * hq * kD * sizeof(float));
+  l.part_o = off;    off = align256(off + (size_t)l.max_dec * hq * kD * sizeof(uint16_t));
   l.total = off;
   return l;
 }
@@ -264,8 +266,8 @@ struct RunArgs {
   const int4* dec_items;
   const int4* comb_seqs;
   const int4* pf_items;
-  float2* part_ml;
-  float* part_o;
+  float2* part_ml;   // per (split, head): running max m (log2 units) and sum l
+  uint16_t* part_o;  // per (split, head, dim): o / l as bf16
   int64_t q_row, q_head;     // element strides
   int64_t kv_row, kv_head;
   int64_t o_row, o_head;
@@ -275,6 +277,13 @@ struct RunArgs {
   float scale_log2;
   int32_t win_left, win_right;
   int32_t grid_dec, grid_pf, grid_comb;  // work items the launch grids cover
+  // Fused KV append of decode rows (k_new == nullptr: none). Row t of k_new / v_new is
+  // the new key / value of packed query row t; it goes to pool row write_slots[t].
+  const uint8_t* k_new;
+  const uint8_t* v_new;
+  const int64_t* write_slots;
+  int64_t kn_row, kn_head, vn_row, vn_head;  // element strides
+  int64_t pool_rows;
 };
 
 // True when the workspace holds a plan for this run's shape; otherwise the block
@@ -447,6 +456,35 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
     }
   }
 
+  // Fused append (decode rows only): the split holding key L-1, this row's new token,
+  // takes that token's K/V from k_new / v_new instead of the pool and writes it to pool
+  // row write_slots[q0] (the 16 lanes owning the token each store their 16-byte chunk
+  // of head g). No other workgroup reads that pool row during this launch.
+  if (a.k_new != nullptr && L >= 1 && L - 1 >= key0 && L - 1 < key0 + kSplit) {
+    const int nn = L - 1 - key0;
+    const bool owner = (nn >> 6) == w && (nn & 3) == r;
+    const int i_new = (nn & 63) >> 2;
+    const uint4 knew = ld16(reinterpret_cast<const T*>(a.k_new) + (int64_t)q0 * a.kn_row +
+                            (int64_t)g * a.kn_head + 8 * c);
+    const uint4 vnew = ld16(reinterpret_cast<const T*>(a.v_new) + (int64_t)q0 * a.vn_row +
+                            (int64_t)g * a.vn_head + 8 * c);
+    if (owner) {
+      const int64_t slot = a.write_slots[q0];
+      if (slot >= 0 && slot < a.pool_rows) {
+        const int64_t off = slot * a.kv_row + (int64_t)g * a.kv_head + 8 * c;
+        *reinterpret_cast<uint4*>(const_cast<uint8_t*>(a.k) + off * (int64_t)sizeof(T)) = knew;
+        *reinterpret_cast<uint4*>(const_cast<uint8_t*>(a.v) + off * (int64_t)sizeof(T)) = vnew;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i == i_new && owner) {
+        kr[i] = knew;
+        vr[i] = vnew;
+      }
+    }
+  }
+
   // q . k on VALU (packed dot2, fp32 accumulate), then the 16 lanes of each row group
   // exchange partial sums so that lane (r, c) ends with token 64w + 4c + r.
   float part[16][G];
@@ -549,7 +587,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
       if (a.lse && d == 0)
         a.lse[(int64_t)qh * a.total_q + q0] = lh > 0.f ? (mh + log2f(lh)) * kLn2 : -INFINITY;
     } else {
-      a.part_o[((int64_t)item * a.hq + qh) * kD + d] = acc;
+      a.part_o[((int64_t)item * a.hq + qh) * kD + d] = hx::Elem<__bf16>::bits(lh > 0.f ? acc / lh : 0.f);
       if (d == 0) a.part_ml[(int64_t)item * a.hq + qh] = make_float2(mh, lh);
     }
   }
@@ -578,7 +616,7 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(RunArgs a) {
     const int h = oi >> 7, d = oi & (kD - 1);
     const int qh = g * G + h;
     const float2* ml = a.part_ml + (int64_t)first * a.hq + qh;
-    const float* po = a.part_o + ((int64_t)first * a.hq + qh) * kD + d;
+    const uint16_t* po = a.part_o + ((int64_t)first * a.hq + qh) * kD + d;
     const int64_t step_o = (int64_t)a.hq * kD;
     float m_run = -INFINITY, l_run = 0.f, acc = 0.f;
     for (int s0 = 0; s0 < splits; s0 += kChunk) {
@@ -588,7 +626,7 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(RunArgs a) {
       for (int j = 0; j < kChunk; ++j) {
         const int sj = s0 + j < splits ? s0 + j : splits - 1;  // clamp: duplicates get weight 0
         mlv[j] = ml[(int64_t)sj * a.hq];
-        ov[j] = po[(int64_t)sj * step_o];
+        ov[j] = __uint_as_float((uint32_t)po[(int64_t)sj * step_o] << 16);
       }
       float cm = m_run;
 #pragma unroll
@@ -601,8 +639,8 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(RunArgs a) {
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
           const bool live = s0 + j < splits && mlv[j].x != -INFINITY;
-          const float wgt = live ? exp2f(mlv[j].x - cm) : 0.f;
-          l_run += wgt * mlv[j].y;
+          const float wgt = live ? exp2f(mlv[j].x - cm) * mlv[j].y : 0.f;  // partial stores o / l
+          l_run += wgt;
           acc += wgt * ov[j];
         }
         m_run = cm;
@@ -960,20 +998,32 @@ int hx_varlen_attn_plan(const int32_t* cu_seq_q, const int32_t* cu_seq_k,
   return hx::status_from_hip(hipGetLastError());
 }
 
-int hx_varlen_attn_run(const void* q, int64_t q_row_stride, int64_t q_head_stride,
-                       const void* k_cache, const void* v_cache,
-                       int64_t kv_row_stride, int64_t kv_head_stride,
-                       int32_t num_pages, int32_t page_size,
-                       const int32_t* block_table, int32_t block_table_stride,
-                       int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
-                       int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
-                       float scale, int32_t window_left, int32_t window_right,
-                       int32_t dtype,
-                       void* out, int64_t o_row_stride, int64_t o_head_stride,
-                       float* lse,
-                       int32_t decode_items_hint, int32_t prefill_items_hint,
-                       int32_t combine_seqs_hint,
-                       void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+struct AppendSpec {
+  const void* k_new;
+  const void* v_new;
+  int64_t kn_row, kn_head, vn_row, vn_head;
+  const int64_t* write_slots;
+  int64_t pool_rows;
+};
+
+int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+             const void* k_cache, const void* v_cache,
+             int64_t kv_row_stride, int64_t kv_head_stride,
+             int32_t num_pages, int32_t page_size,
+             const int32_t* block_table, int32_t block_table_stride,
+             int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+             int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+             float scale, int32_t window_left, int32_t window_right,
+             int32_t dtype,
+             void* out, int64_t o_row_stride, int64_t o_head_stride,
+             float* lse,
+             int32_t decode_items_hint, int32_t prefill_items_hint,
+             int32_t combine_seqs_hint,
+             void* workspace, size_t workspace_bytes, void* stream, const AppendSpec* app) {
   int st = check_shape(batch, max_q, max_k, n_q_heads, n_kv_heads, head_dim);
   if (st != HX_OK) return st;
   if (dtype != HX_DTYPE_BF16 && dtype != HX_DTYPE_FP16) return HX_E_UNSUPPORTED;
@@ -1009,7 +1059,7 @@ int hx_varlen_attn_run(const void* q, int64_t q_row_stride, int64_t q_head_strid
   a.comb_seqs = reinterpret_cast<const int4*>(ws + l.comb_seqs);
   a.pf_items = reinterpret_cast<const int4*>(ws + l.pf_items);
   a.part_ml = reinterpret_cast<float2*>(ws + l.part_ml);
-  a.part_o = reinterpret_cast<float*>(ws + l.part_o);
+  a.part_o = reinterpret_cast<uint16_t*>(ws + l.part_o);
   a.q_row = q_row_stride;
   a.q_head = q_head_stride;
   a.kv_row = kv_row_stride;
@@ -1037,10 +1087,97 @@ int hx_varlen_attn_run(const void* q, int64_t q_row_stride, int64_t q_head_strid
   a.grid_comb = clamp_hint(combine_seqs_hint, batch);
   if ((int64_t)a.grid_dec * n_kv_heads > INT32_MAX || (int64_t)a.grid_pf * n_kv_heads > INT32_MAX)
     return HX_E_INVALID_ARG;
-  const int G = n_q_heads / n_kv_heads;
+  a.k_new = nullptr;
+  a.v_new = nullptr;
+  a.write_slots = nullptr;
+  a.kn_row = a.kn_head = a.vn_row = a.vn_head = 0;
+  a.pool_rows = 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (app != nullptr && total_q > 0) {
+    if (!app->k_new || !app->v_new || !app->write_slots) return HX_E_INVALID_ARG;
+    if ((uintptr_t)app->k_new % 16 || (uintptr_t)app->v_new % 16 || app->kn_row % 8 ||
+        app->kn_head % 8 || app->vn_row % 8 || app->vn_head % 8 || app->kn_row < 0 ||
+        app->kn_head < 0 || app->vn_row < 0 || app->vn_head < 0 || app->pool_rows < 0)
+      return HX_E_INVALID_ARG;
+    // Chunk rows read their own new keys from the pool: append every row first.
+    if (a.grid_pf > 0) {
+      const int elem = 2;
+      const int st2 = hx_kv_append(const_cast<void*>(k_cache), const_cast<void*>(v_cache), app->pool_rows,
+                                   app->k_new, app->kn_row, app->kn_head, app->v_new, app->vn_row,
+                                   app->vn_head, app->write_slots, total_q, n_kv_heads, head_dim, elem,
+                                   stream);
+      if (st2 != HX_OK) return st2;
+    }
+    a.k_new = static_cast<const uint8_t*>(app->k_new);
+    a.v_new = static_cast<const uint8_t*>(app->v_new);
+    a.write_slots = app->write_slots;
+    a.kn_row = app->kn_row;
+    a.kn_head = app->kn_head;
+    a.vn_row = app->vn_row;
+    a.vn_head = app->vn_head;
+    a.pool_rows = app->pool_rows;
+  }
+  const int G = n_q_heads / n_kv_heads;
   if (dtype == HX_DTYPE_BF16) return launch_run_g<__bf16>(a, G, s);
   return launch_run_g<_Float16>(a, G, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int hx_varlen_attn_run(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                       const void* k_cache, const void* v_cache,
+                       int64_t kv_row_stride, int64_t kv_head_stride,
+                       int32_t num_pages, int32_t page_size,
+                       const int32_t* block_table, int32_t block_table_stride,
+                       int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                       int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                       float scale, int32_t window_left, int32_t window_right,
+                       int32_t dtype,
+                       void* out, int64_t o_row_stride, int64_t o_head_stride,
+                       float* lse,
+                       int32_t decode_items_hint, int32_t prefill_items_hint,
+                       int32_t combine_seqs_hint,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  return run_impl(q, q_row_stride, q_head_stride, k_cache, v_cache, kv_row_stride, kv_head_stride,
+                  num_pages, page_size, block_table, block_table_stride, batch, total_q, max_q,
+                  max_k, n_q_heads, n_kv_heads, head_dim, scale, window_left, window_right, dtype,
+                  out, o_row_stride, o_head_stride, lse, decode_items_hint, prefill_items_hint,
+                  combine_seqs_hint, workspace, workspace_bytes, stream, nullptr);
+}
+
+int hx_varlen_attn_append_run(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                              void* k_cache, void* v_cache,
+                              int64_t kv_row_stride, int64_t kv_head_stride,
+                              int32_t num_pages, int32_t page_size,
+                              const int32_t* block_table, int32_t block_table_stride,
+                              int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                              int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                              float scale, int32_t window_left, int32_t window_right,
+                              int32_t dtype,
+                              void* out, int64_t o_row_stride, int64_t o_head_stride,
+                              float* lse,
+                              const void* k_new, int64_t k_new_row_stride, int64_t k_new_head_stride,
+                              const void* v_new, int64_t v_new_row_stride, int64_t v_new_head_stride,
+                              const int64_t* write_slots, int64_t pool_rows,
+                              int32_t decode_items_hint, int32_t prefill_items_hint,
+                              int32_t combine_seqs_hint,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  AppendSpec app;
+  app.k_new = k_new;
+  app.v_new = v_new;
+  app.kn_row = k_new_row_stride;
+  app.kn_head = k_new_head_stride;
+  app.vn_row = v_new_row_stride;
+  app.vn_head = v_new_head_stride;
+  app.write_slots = write_slots;
+  app.pool_rows = pool_rows;
+  return run_impl(q, q_row_stride, q_head_stride, k_cache, v_cache, kv_row_stride, kv_head_stride,
+                  num_pages, page_size, block_table, block_table_stride, batch, total_q, max_q,
+                  max_k, n_q_heads, n_kv_heads, head_dim, scale, window_left, window_right, dtype,
+                  out, o_row_stride, o_head_stride, lse, decode_items_hint, prefill_items_hint,
+                  combine_seqs_hint, workspace, workspace_bytes, stream, &app);
 }
 
 int hx_varlen_attn(const void* q, int64_t q_row_stride, int64_t q_head_stride,

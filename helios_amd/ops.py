@@ -71,6 +71,23 @@ def kv_append(
     strides). ``write_slots``: int64 ``[T]`` flat slot ids (page * page_size + offset).
     """
     device = _require_gpu(k_cache, v_cache, write_slots, keys, values)
+    _check_append(k_cache, v_cache, write_slots, keys, values)
+    n_kv, head_dim = keys.shape[1], keys.shape[2]
+    write_slots = write_slots.contiguous()
+    pool_rows = k_cache.numel() // (n_kv * head_dim)
+    code = _capi.lib().hx_kv_append(
+        k_cache.data_ptr(), v_cache.data_ptr(), pool_rows,
+        keys.data_ptr(), keys.stride(0), keys.stride(1),
+        values.data_ptr(), values.stride(0), values.stride(1),
+        write_slots.data_ptr(), keys.shape[0],
+        n_kv, head_dim, _elem_bytes(keys),
+        _stream_ptr(device),
+    )
+    _capi.check(code, "hx_kv_append")
+
+
+def _check_append(k_cache, v_cache, write_slots, keys, values) -> None:
+    """Argument checks shared by kv_append and the fused append path."""
     if k_cache.shape != v_cache.shape or k_cache.dtype != v_cache.dtype:
         raise ValueError("Key and value pools must have identical shapes and dtypes.")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
@@ -86,17 +103,6 @@ def kv_append(
         raise ValueError("write_slots must be int64 [tokens].")
     if keys.stride(2) != 1 or values.stride(2) != 1:
         raise ValueError("Appended K/V must have a contiguous head_dim.")
-    write_slots = write_slots.contiguous()
-    pool_rows = k_cache.numel() // (n_kv * head_dim)
-    code = _capi.lib().hx_kv_append(
-        k_cache.data_ptr(), v_cache.data_ptr(), pool_rows,
-        keys.data_ptr(), keys.stride(0), keys.stride(1),
-        values.data_ptr(), values.stride(0), values.stride(1),
-        write_slots.data_ptr(), keys.shape[0],
-        n_kv, head_dim, _elem_bytes(keys),
-        _stream_ptr(device),
-    )
-    _capi.check(code, "hx_kv_append")
 
 
 # --------------------------------------------------------------------- page copy
@@ -294,10 +300,16 @@ class VarlenAttnPlan:
         out: torch.Tensor | None = None,
         return_lse: bool = False,
         phases: tuple[str, ...] = ("decode", "combine", "chunk"),
+        append: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
     ) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
         """Attention for one layer. ``phases`` launches a subset of the three kernels
         (decode splits, split combine, chunk rows); a full result needs all three, in
-        that order, into the same ``out``. Profilers use it to time each kernel."""
+        that order, into the same ``out``. Profilers use it to time each kernel.
+
+        ``append=(k_new, v_new, write_slots)`` first writes the tick's new K/V rows
+        into the pool (index_copy_ semantics, as ``kv_append``) in the same call: decode
+        rows inside the decode kernel, chunk rows by the append kernel beforehand.
+        """
         _require_gpu(query, k_cache, v_cache)
         unknown = set(phases) - {"decode", "combine", "chunk"}
         if unknown:
@@ -343,7 +355,12 @@ class VarlenAttnPlan:
         if return_lse:
             lse = torch.empty((self.n_q_heads, self.total_q), dtype=torch.float32, device=query.device)
         scale = 1.0 / math.sqrt(self.head_dim) if scale is None else float(scale)
-        code = _capi.lib().hx_varlen_attn_run(
+        hints = (
+            self.hints[0] if "decode" in phases else 0,
+            self.hints[1] if "chunk" in phases else 0,
+            self.hints[2] if "combine" in phases else 0,
+        )
+        common = (
             query.data_ptr(), query.stride(0), query.stride(1),
             k_cache.data_ptr(), v_cache.data_ptr(), row_stride, head_stride,
             num_pages, self.page_size,
@@ -353,12 +370,27 @@ class VarlenAttnPlan:
             scale, self.window[0], self.window[1], _SUPPORTED[query.dtype],
             out.data_ptr(), out.stride(0), out.stride(1),
             None if lse is None else lse.data_ptr(),
-            self.hints[0] if "decode" in phases else 0,
-            self.hints[1] if "chunk" in phases else 0,
-            self.hints[2] if "combine" in phases else 0,
-            self.ws_ptr, self.ws_bytes, _stream_ptr(query.device),
         )
-        _capi.check(code, "hx_varlen_attn_run")
+        if append is None:
+            code = _capi.lib().hx_varlen_attn_run(
+                *common, *hints, self.ws_ptr, self.ws_bytes, _stream_ptr(query.device))
+            _capi.check(code, "hx_varlen_attn_run")
+        else:
+            k_new, v_new, slots = append
+            _check_append(k_cache, v_cache, slots, k_new, v_new)
+            if k_new.shape[0] != self.total_q:
+                raise ValueError("append rows must match the packed query rows.")
+            if not k_cache.is_contiguous() or not v_cache.is_contiguous():
+                raise ValueError("KV pools must be contiguous.")
+            pool_rows = k_cache.numel() // (self.n_kv_heads * self.head_dim)
+            slots = slots.contiguous()
+            code = _capi.lib().hx_varlen_attn_append_run(
+                *common,
+                k_new.data_ptr(), k_new.stride(0), k_new.stride(1),
+                v_new.data_ptr(), v_new.stride(0), v_new.stride(1),
+                slots.data_ptr(), pool_rows,
+                *hints, self.ws_ptr, self.ws_bytes, _stream_ptr(query.device))
+            _capi.check(code, "hx_varlen_attn_append_run")
         return (out, lse) if return_lse else out
 
 

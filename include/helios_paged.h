@@ -176,6 +176,37 @@ int hx_varlen_attn_run(const void* q, int64_t q_row_stride, int64_t q_head_strid
                        int32_t combine_seqs_hint,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * KV append + attention in one call: the PagedBatchCache.attend sequence of the
+ * reference (paged_cache.py:301-332 and :501-520: _write, i.e. index_copy_ of the new
+ * rows into k_cache / v_cache at write_slots, then varlen_attn on the updated pool).
+ * Row t of k_new / v_new ([total_q, n_kv_heads, head_dim], strides in elements) is
+ * the new key / value of packed query row t. Decode rows are appended inside the
+ * decode kernel (the workgroup owning the row's last split stores its head's slice
+ * and uses it from registers), so a decode-only tick issues no separate append
+ * launch; when chunk rows are present every row is appended first by the append
+ * kernel. The pool must hold the token of decode row b at block-table position
+ * seqused_k[b] - 1, i.e. write_slots must agree with the block table, as the
+ * reference's metadata does by construction. pool_rows = num_pages * page_size.
+ */
+int hx_varlen_attn_append_run(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                              void* k_cache, void* v_cache,
+                              int64_t kv_row_stride, int64_t kv_head_stride,
+                              int32_t num_pages, int32_t page_size,
+                              const int32_t* block_table, int32_t block_table_stride,
+                              int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                              int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                              float scale, int32_t window_left, int32_t window_right,
+                              int32_t dtype,
+                              void* out, int64_t o_row_stride, int64_t o_head_stride,
+                              float* lse,
+                              const void* k_new, int64_t k_new_row_stride, int64_t k_new_head_stride,
+                              const void* v_new, int64_t v_new_row_stride, int64_t v_new_head_stride,
+                              const int64_t* write_slots, int64_t pool_rows,
+                              int32_t decode_items_hint, int32_t prefill_items_hint,
+                              int32_t combine_seqs_hint,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
 int hx_varlen_attn(const void* q, int64_t q_row_stride, int64_t q_head_stride,
                    const void* k_cache, const void* v_cache,
                    int64_t kv_row_stride, int64_t kv_head_stride,

@@ -173,3 +173,29 @@ def test_validation_errors(device):
         ops.varlen_attn(tick.q, tick.k_pool, tick.v_pool, tick.cu_seq_q, tick.cu_seq_k, w.max_q,
                         w.max_k, enable_gqa=True, seqused_k=tick.seqused_k,
                         block_table=tick.block_table.long())
+
+
+@pytest.mark.parametrize("name", ["c1", "mixed"])
+def test_fused_append_matches_separate_calls(device, name):
+    say("fused append", name)
+    w = synth.c1() if name == "c1" else synth.small_mixed(80, batch=7, max_cached=1500, max_chunk=300,
+                                                           num_pages=64)
+    dtype = torch.bfloat16
+    ref = DeviceTick(w, dtype, device)          # pools already hold the appended rows
+    out_ref = ref.attend(exact_grid=True)
+    # the same inputs before the append
+    s = w.seed * 7919
+    shape = (w.num_pages, w.page_size, w.n_kv_heads, w.head_dim)
+    k_pool = torch.from_numpy(synth.normal(s + 4, shape)).to(dtype).to(device)
+    v_pool = torch.from_numpy(synth.normal(s + 5, shape)).to(dtype).to(device)
+    plan = ops.VarlenAttnPlan(
+        ref.cu_seq_q, ref.cu_seq_k, ref.seqused_k, total_q=w.total_q, max_q=w.max_q, max_k=w.max_k,
+        n_q_heads=w.n_q_heads, n_kv_heads=w.n_kv_heads, head_dim=w.head_dim, page_size=w.page_size,
+        block_table_stride=ref.block_table.shape[1], q_lens=w.q_lens, k_lens=w.k_lens)
+    out = plan.run(ref.q, k_pool, v_pool, ref.block_table,
+                   append=(ref.k_new, ref.v_new, ref.write_slots))
+    torch.cuda.synchronize()
+    assert plan.error_word() == 0
+    assert torch.equal(k_pool.view(torch.int16), ref.k_pool.view(torch.int16))
+    assert torch.equal(v_pool.view(torch.int16), ref.v_pool.view(torch.int16))
+    assert torch.equal(out, out_ref)
