@@ -21,6 +21,8 @@ Printed JSON (one line):
   packed_tick  the mixed tick (32 decoders + 1024- and 992-token chunks): one layer's
             append + attention time, and tokens/s of 36 such layers (attention and KV
             work only; the model's GEMMs are not part of this path).
+  long_context  the long-context tick (8 x 32768 keys with a shared 16-page prefix +
+            a 4096-token chunk) and the 36-layer restore copy of 16 prefix pages.
   cpu_baseline  the reference's dense-KV path (gather, repeat_interleave, SDPA) in
             torch fp32 on the host cores, on one full decode layer of the same tick.
 """
@@ -200,6 +202,60 @@ def packed_tick(device, steps: int = 30, warmup: int = 5):
     return res
 
 
+def long_context(device, steps: int = 10, warmup: int = 3):
+    """The long-context tick: 8 decoders at 32768 keys whose first 16 pages are shared,
+    plus one 4096-token chunk at positions 4096-8191; and the restore of 16 prefix pages
+    (K and V of all 36 layers) by page copy."""
+    import torch
+
+    from helios_amd import ops, synth
+
+    w = synth.c4()
+    b = DecodeBench(w, device, copies=1)
+    for _ in range(warmup):
+        b.step(0)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    for i in range(steps):
+        b.step(0, ev[i])
+    torch.cuda.synchronize()
+    append_us = statistics.mean(e[0].elapsed_time(e[1]) for e in ev) * 1e3
+    decode_us = statistics.mean(e[1].elapsed_time(e[2]) for e in ev) * 1e3
+    chunk_us = statistics.mean(e[2].elapsed_time(e[3]) for e in ev) * 1e3
+    del b
+    torch.cuda.empty_cache()
+    # restore copy: 16 prefix pages of every layer, keys and values
+    layers, n = N_LAYERS_MODEL, 16
+    shape = (2 * n, w.page_size, w.n_kv_heads, w.head_dim)
+    kl = [torch.randn(shape, device=device, dtype=torch.bfloat16) for _ in range(layers)]
+    vl = [torch.randn(shape, device=device, dtype=torch.bfloat16) for _ in range(layers)]
+    src, dst = list(range(n)), list(range(n, 2 * n))
+    for _ in range(3):
+        ops.kv_copy_pages(kl, vl, src, dst)
+    cev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(10)]
+    for a_, b_ in cev:
+        a_.record()
+        ops.kv_copy_pages(kl, vl, src, dst)
+        b_.record()
+    torch.cuda.synchronize()
+    copy_us = statistics.median(a_.elapsed_time(b_) for a_, b_ in cev) * 1e3
+    copy_bytes = 2 * layers * 2 * n * kl[0][0].numel() * 2
+    assert torch.equal(kl[5][dst[3]], kl[5][src[3]]) and torch.equal(vl[35][dst[0]], vl[35][src[0]])
+    del kl, vl
+    torch.cuda.empty_cache()
+    return {
+        "workload": "c4: 8 decoders x 32768 keys (first 16 pages shared) + chunk 4096 rows at "
+                    "positions 4096-8191; restore of 16 prefix pages x 36 layers x K/V",
+        "append_us": round(append_us, 2),
+        "decode_rows_us": round(decode_us, 2),
+        "decode_rows_gbs_unique": round(w.decode_bytes() / (decode_us * 1e-6) / 1e9, 1),
+        "chunk_rows_us": round(chunk_us, 2),
+        "chunk_rows_tflops": round(w.chunk_flops() / (chunk_us * 1e-6) / 1e12, 1),
+        "chunk_mfma_frac": round(w.chunk_flops() / (chunk_us * 1e-6) / 2.5e15, 4),
+        "restore_copy_us": round(copy_us, 2),
+        "restore_copy_gbs_rw": round(copy_bytes / (copy_us * 1e-6) / 1e9, 1),
+    }
+
+
 def pmc_pass(device):
     """Counter-collection run: a page copy of known size, then decode steps."""
     import torch
@@ -314,6 +370,7 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_packed_tick:
         result["packed_tick"] = packed_tick(device)
+        result["long_context"] = long_context(device)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)
