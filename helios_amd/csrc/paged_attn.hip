@@ -21,10 +21,10 @@
 //                   halved; the extra error is one more bf16 rounding of the output).
 //   combine_kernel  merges the partials of each long decode sequence in split order, so
 //                   results do not depend on scheduling.
-//   chunk_kernel    prefill chunks: 4 waves per workgroup, each wave owning 64 query rows
-//                   of one head; 64-key K / V^T tiles go through LDS with a register
-//                   prefetch of the next tile; S^T = K Q^T and O^T = V^T P^T both run on
-//                   16x16x32 MFMA with online softmax in between.
+//   chunk_kernel    prefill chunks: 8 waves per workgroup (2 per SIMD), each wave owning
+//                   32 query rows of one head; 64-key K / V^T tiles go through LDS with a
+//                   register prefetch of the next tile; S^T = K Q^T and O^T = V^T P^T both
+//                   run on 16x16x32 MFMA with online softmax in between.
 
 #include "hx_common.h"
 
@@ -656,13 +656,19 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(RunArgs a) {
 // ------------------------------------------------------------------ chunk (prefill) MFMA
 constexpr int kKStride = kD + 8;       // K tile row: 136 elements (272 B)
 constexpr int kVStride = kTile + 4;    // V^T tile row: 68 elements (136 B)
+constexpr int kChunkThreads = 512;     // 8 waves: 2 per SIMD
 
+// One workgroup per (sequence, block of 256/Gw query rows, group of Gw <= 4 query
+// heads of KV head g). Wave w owns 32 rows (two 16-row MFMA blocks) of head w % Gw.
+// Each 64-key tile of K (row-major) and V (transposed, key pairs packed per 32-bit
+// word) goes through LDS once and feeds all 8 waves; the next tile is prefetched into
+// registers while the current one is consumed. Two waves per SIMD hide each other's
+// LDS and memory latency.
 template <typename T, int G>
-__global__ __launch_bounds__(kThreads, 1) void chunk_kernel(RunArgs a) {
+__global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   typedef hx::Elem<T> E;
   typedef typename E::v8 v8;
   constexpr int Gw = G < 4 ? G : 4;
-  constexpr int R = 4 / Gw;
   __shared__ __attribute__((aligned(16))) T k_lds[kTile * kKStride];
   __shared__ __attribute__((aligned(16))) T vt_lds[kD * kVStride];
 
@@ -680,7 +686,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(RunArgs a) {
   const int4 si = a.seq_info[b];
   const int q0 = si.x, n = si.y, L = si.z, kvb = si.w;
   const int off = L - n;  // key position of query row 0
-  const int wg_row_end = min(n, row0 + 64 * R);
+  const int wg_row_end = min(n, row0 + 32 * (8 / Gw));
 
   int klo = 0;
   if (a.win_left >= 0) klo = max(0, off + row0 - a.win_left);
@@ -689,13 +695,14 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(RunArgs a) {
   const int t_begin = klo / kTile;
   const int t_end = khi >= klo ? khi / kTile + 1 : t_begin;
 
-  const int wr0 = row0 + 64 * (w / Gw);
+  const int wr0 = row0 + 32 * (w / Gw);
   const int qh = g * G + hquad * Gw + (w % Gw);
+  const float sl2 = a.scale_log2;
 
   // Q^T as the MFMA B operand: lane holds row wr0+16rb+(lane&15), dims 32st+8(lane>>4)..+7.
-  uint4 qf[4][4];
+  uint4 qf[2][4];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
+  for (int rb = 0; rb < 2; ++rb) {
     const int rr = wr0 + 16 * rb + (lane & 15);
     const bool ok = rr < n;
     const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)(q0 + (ok ? rr : 0)) * a.q_row +
@@ -704,18 +711,18 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(RunArgs a) {
     for (int st = 0; st < 4; ++st) qf[rb][st] = ok ? ld16(qp + 32 * st) : hx::zero4();
   }
 
-  hx::f32x4_t oacc[8][4];
+  hx::f32x4_t oacc[8][2];
 #pragma unroll
   for (int db = 0; db < 8; ++db)
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) oacc[db][rb] = hx::f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  float l_run[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int rb = 0; rb < 2; ++rb) oacc[db][rb] = hx::f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY};  // running row max of the raw scores
+  float l_run[2] = {0.f, 0.f};              // this lane's share of the row sum
 
   const int c16 = tid & 15;     // 16-byte chunk of a key row this thread moves
-  const int kr_base = tid >> 4; // 0..15
+  const int kr_base = tid >> 4; // 0..31
 
-  uint4 kreg[4], vreg[4];
+  uint4 kreg[2], vreg[2];
   auto load_tile = [&](int t) {
     const int key_base = t * kTile;
     int64_t rowb;
@@ -732,10 +739,10 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(RunArgs a) {
     const T* vp = reinterpret_cast<const T*>(a.v) + rowb * a.kv_row + (int64_t)g * a.kv_head + 8 * c16;
     const int kvr = (int)a.kv_row;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int kk = kr_base + 16 * j;
+    for (int j = 0; j < 2; ++j) {
+      const int kk = kr_base + 32 * j;
       kreg[j] = (ok_page && key_base + kk < L) ? ld16(kp + kk * kvr) : hx::zero4();
-      const int vk = 2 * kr_base + (j & 1) + 32 * (j >> 1);
+      const int vk = 2 * kr_base + j;
       vreg[j] = (ok_page && key_base + vk < L) ? ld16(vp + vk * kvr) : hx::zero4();
     }
   };
@@ -744,12 +751,11 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(RunArgs a) {
   for (int t = t_begin; t < t_end; ++t) {
     // Registers -> LDS: K row-major, V transposed (pairs of keys packed per 32-bit word).
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<uint4*>(&k_lds[(kr_base + 16 * j) * kKStride + 8 * c16]) = kreg[j];
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const uint4 x = vreg[2 * jj], y = vreg[2 * jj + 1];
-      const int kp2 = 2 * kr_base + 32 * jj;
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<uint4*>(&k_lds[(kr_base + 32 * j) * kKStride + 8 * c16]) = kreg[j];
+    {
+      const uint4 x = vreg[0], y = vreg[1];
+      const int kp2 = 2 * kr_base;
       const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
       const uint32_t ys[4] = {y.x, y.y, y.z, y.w};
 #pragma unroll
@@ -764,11 +770,11 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(RunArgs a) {
 
     const int t0 = t * kTile;
     // S^T = K Q^T: lane holds keys 16kb+4(lane>>4)+i of row 16rb+(lane&15).
-    hx::f32x4_t sacc[4][4];
+    hx::f32x4_t sacc[4][2];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) sacc[kb][rb] = hx::f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int rb = 0; rb < 2; ++rb) sacc[kb][rb] = hx::f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
 #pragma unroll
@@ -776,55 +782,57 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(RunArgs a) {
         const uint4 af = *reinterpret_cast<const uint4*>(
             &k_lds[(16 * kb + (lane & 15)) * kKStride + 32 * st + 8 * (lane >> 4)]);
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
+        for (int rb = 0; rb < 2; ++rb)
           sacc[kb][rb] = E::mfma16x16x32(hx::as_v8<T>(af), hx::as_v8<T>(qf[rb][st]), sacc[kb][rb]);
       }
     }
 
     // Mask only where the tile is not fully visible to every row of this wave.
-    bool full = (n - wr0 >= 64) && (t0 + kTile - 1 <= L - 1);
-    if (a.win_left >= 0) full = full && (off + wr0 + 63 - a.win_left <= t0);
+    bool full = (n - wr0 >= 32) && (t0 + kTile - 1 <= L - 1);
+    if (a.win_left >= 0) full = full && (off + wr0 + 31 - a.win_left <= t0);
     if (a.win_right >= 0) full = full && (off + wr0 + a.win_right >= t0 + kTile - 1);
 
-    v8 pb[2][4];
+    v8 pb[2][2];
+    float alpha[2];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
+    for (int rb = 0; rb < 2; ++rb) {
       const int rr = wr0 + 16 * rb + (lane & 15);
-      const int qpos = off + rr;
-      int rlo = a.win_left >= 0 ? qpos - a.win_left : -2147483647;
-      int rhi = L - 1;
-      if (a.win_right >= 0) rhi = min(rhi, qpos + a.win_right);
-      if (rr >= n) rhi = -1;
-      float mx = -INFINITY;
+      if (!full) {
+        const int qpos = off + rr;
+        const int rlo = a.win_left >= 0 ? qpos - a.win_left : -2147483647;
+        int rhi = L - 1;
+        if (a.win_right >= 0) rhi = min(rhi, qpos + a.win_right);
+        if (rr >= n) rhi = -1;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float v = sacc[kb][rb][i] * a.scale_log2;
-          if (!full) {
+          for (int i = 0; i < 4; ++i) {
             const int key = t0 + 16 * kb + 4 * (lane >> 4) + i;
-            if (key < rlo || key > rhi) v = -INFINITY;
+            if (key < rlo || key > rhi) sacc[kb][rb][i] = -INFINITY;
           }
-          sacc[kb][rb][i] = v;
-          mx = fmaxf(mx, v);
-        }
+      }
+      // Row max on raw scores (the scale is positive), folded into exp2 by one FMA.
+      float mx = fmaxf(fmaxf(sacc[0][rb][0], sacc[0][rb][1]), fmaxf(sacc[0][rb][2], sacc[0][rb][3]));
+#pragma unroll
+      for (int kb = 1; kb < 4; ++kb)
+        mx = fmaxf(mx, fmaxf(fmaxf(sacc[kb][rb][0], sacc[kb][rb][1]), fmaxf(sacc[kb][rb][2], sacc[kb][rb][3])));
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_run[rb], mx);
-      const float alpha = m_new == -INFINITY ? 1.f : exp2f(m_run[rb] - m_new);
+      const bool live = m_new != -INFINITY;
+      alpha[rb] = (live && m_run[rb] != -INFINITY) ? exp2f((m_run[rb] - m_new) * sl2) : (live ? 0.f : 1.f);
+      const float neg_m = live ? -m_new * sl2 : 0.f;
       float psum = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = m_new == -INFINITY ? 0.f : exp2f(sacc[kb][rb][i] - m_new);
+          const float p = exp2f(fmaf(sacc[kb][rb][i], sl2, neg_m));  // -inf -> 0
           sacc[kb][rb][i] = p;
           psum += p;
         }
-      l_run[rb] = l_run[rb] * alpha + psum;
+      l_run[rb] = l_run[rb] * alpha[rb] + psum;
       m_run[rb] = m_new;
-#pragma unroll
-      for (int db = 0; db < 8; ++db) oacc[db][rb] *= alpha;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         uint16_t h8[8];
@@ -838,6 +846,14 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(RunArgs a) {
         pb[ks][rb] = hx::as_v8<T>(u);
       }
     }
+    // Rescale the accumulators only when some row's max moved (after the first tiles of
+    // a row this is rare).
+    if (__any(alpha[0] != 1.f || alpha[1] != 1.f)) {
+#pragma unroll
+      for (int db = 0; db < 8; ++db)
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) oacc[db][rb] *= alpha[rb];
+    }
 
     // O^T += V^T P^T with the key order of pb: {4(lane>>4)+0..3, 16+4(lane>>4)+0..3}.
 #pragma unroll
@@ -849,7 +865,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(RunArgs a) {
         const uint2 hi8 = *reinterpret_cast<const uint2*>(vrow + 16);
         const v8 af = hx::as_v8<T>(make_uint4(lo8.x, lo8.y, hi8.x, hi8.y));
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) oacc[db][rb] = E::mfma16x16x32(af, pb[ks][rb], oacc[db][rb]);
+        for (int rb = 0; rb < 2; ++rb) oacc[db][rb] = E::mfma16x16x32(af, pb[ks][rb], oacc[db][rb]);
       }
     }
     __syncthreads();
@@ -857,7 +873,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(RunArgs a) {
 
   // Normalise and store: lane holds dims 16db+4(lane>>4)+0..3 of row 16rb+(lane&15).
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
+  for (int rb = 0; rb < 2; ++rb) {
     float l = l_run[rb];
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
@@ -873,7 +889,8 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(RunArgs a) {
         *reinterpret_cast<uint2*>(orow + d0) = u;
       }
       if (a.lse && (lane >> 4) == 0)
-        a.lse[(int64_t)qh * a.total_q + q0 + rr] = l > 0.f ? (m_run[rb] + log2f(l)) * kLn2 : -INFINITY;
+        a.lse[(int64_t)qh * a.total_q + q0 + rr] =
+            l > 0.f ? (m_run[rb] * sl2 + log2f(l)) * kLn2 : -INFINITY;
     }
   }
 }
@@ -888,7 +905,7 @@ int launch_run(const RunArgs& a, hipStream_t s) {
   if (a.grid_comb > 0)
     hipLaunchKernelGGL((combine_kernel<T, G>), dim3((unsigned)(a.grid_comb * a.hkv)), dim3(kThreads), 0, s, a);
   if (a.grid_pf > 0)
-    hipLaunchKernelGGL((chunk_kernel<T, G>), dim3((unsigned)(a.grid_pf * a.hkv)), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((chunk_kernel<T, G>), dim3((unsigned)(a.grid_pf * a.hkv)), dim3(kChunkThreads), 0, s, a);
   return hx::status_from_hip(hipGetLastError());
 }
 
