@@ -59,6 +59,26 @@ struct Elem<_Float16> {
   }
 };
 
+// 2^x with the raw v_exp_f32 (exp2f adds denormal-range fix-ups around it). Softmax
+// arguments are <= 0; results below 2^-126 flush to zero and 2^-inf is 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Two floats rounded to nearest-even and packed as {lo, hi} 16-bit elements.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2_round(float lo, float hi);
+template <>
+__device__ __forceinline__ uint32_t pack2_round<__bf16>(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, b2));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2_round<_Float16>(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, h2));
+}
+
 template <typename T>
 __device__ __forceinline__ typename Elem<T>::v8 as_v8(uint4 u) {
   return __builtin_bit_cast(typename Elem<T>::v8, u);

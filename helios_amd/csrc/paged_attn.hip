@@ -512,7 +512,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     const float m = fmaxf(fmaxf(red_max[0][h], red_max[1][h]), fmaxf(red_max[2][h], red_max[3][h]));
-    const float p = sc[h] == -INFINITY ? 0.f : exp2f(sc[h] - m);
+    const float p = sc[h] == -INFINITY ? 0.f : hx::fast_exp2(sc[h] - m);
     sc[h] = p;
     ps[h] = wave_sum(p);
   }
@@ -633,13 +633,13 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(RunArgs a) {
       for (int j = 0; j < kChunk; ++j)
         if (s0 + j < splits) cm = fmaxf(cm, mlv[j].x);
       if (cm != -INFINITY) {
-        const float rescale = m_run == -INFINITY ? 0.f : exp2f(m_run - cm);
+        const float rescale = m_run == -INFINITY ? 0.f : hx::fast_exp2(m_run - cm);
         l_run *= rescale;
         acc *= rescale;
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
           const bool live = s0 + j < splits && mlv[j].x != -INFINITY;
-          const float wgt = live ? exp2f(mlv[j].x - cm) * mlv[j].y : 0.f;  // partial stores o / l
+          const float wgt = live ? hx::fast_exp2(mlv[j].x - cm) * mlv[j].y : 0.f;  // partial stores o / l
           l_run += wgt;
           acc += wgt * ov[j];
         }
@@ -722,16 +722,38 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   const int c16 = tid & 15;     // 16-byte chunk of a key row this thread moves
   const int kr_base = tid >> 4; // 0..31
 
+  // Page ids of the key range, 64 at a time: lane j holds the id of page pg_base + j,
+  // so a tile finds its page with one v_readlane instead of a dependent global load.
+  const bool paged = a.page_size > 0;
+  const int last_pg = paged && khi >= 0 ? khi / a.page_size : -1;
+  int pg_base = paged ? (t_begin * kTile) / a.page_size : 0;
+  int pg_ids = -1;
+  auto fetch_pages = [&]() {
+    const int p = pg_base + lane;
+    pg_ids = p <= last_pg ? a.bt[(int64_t)b * a.bt_stride + p] : -1;
+  };
+  if (paged) fetch_pages();
+
+  // Key rows past L - 1 (only in the last tile) load row L - 1 instead, which lies in the
+  // same page; their scores are masked to -inf, so no branch guards the loads. A bad page
+  // id reads page 0 and is reported in the error word.
   uint4 kreg[2], vreg[2];
   auto load_tile = [&](int t) {
     const int key_base = t * kTile;
+    const int kmax = min(L - 1 - key_base, kTile - 1);  // >= 0: key_base <= khi <= L - 1
     int64_t rowb;
-    bool ok_page = true;
-    if (a.page_size > 0) {
-      const int page = a.bt[(int64_t)b * a.bt_stride + key_base / a.page_size];
-      ok_page = page >= 0 && page < a.num_pages;
-      if (!ok_page && tid == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_BAD_PAGE);
-      rowb = (int64_t)(ok_page ? page : 0) * a.page_size + key_base % a.page_size;
+    if (paged) {
+      const int pi = key_base / a.page_size;
+      if (pi - pg_base >= 64) {
+        pg_base = pi;
+        fetch_pages();
+      }
+      int page = __builtin_amdgcn_readlane(pg_ids, pi - pg_base);
+      if ((unsigned)page >= (unsigned)a.num_pages) {
+        if (tid == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_BAD_PAGE);
+        page = 0;
+      }
+      rowb = (int64_t)page * a.page_size + (key_base - pi * a.page_size);
     } else {
       rowb = (int64_t)kvb + key_base;
     }
@@ -740,10 +762,8 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
     const int kvr = (int)a.kv_row;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int kk = kr_base + 32 * j;
-      kreg[j] = (ok_page && key_base + kk < L) ? ld16(kp + kk * kvr) : hx::zero4();
-      const int vk = 2 * kr_base + j;
-      vreg[j] = (ok_page && key_base + vk < L) ? ld16(vp + vk * kvr) : hx::zero4();
+      kreg[j] = ld16(kp + min(kr_base + 32 * j, kmax) * kvr);
+      vreg[j] = ld16(vp + min(2 * kr_base + j, kmax) * kvr);
     }
   };
 
@@ -820,14 +840,15 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_run[rb], mx);
       const bool live = m_new != -INFINITY;
-      alpha[rb] = (live && m_run[rb] != -INFINITY) ? exp2f((m_run[rb] - m_new) * sl2) : (live ? 0.f : 1.f);
+      alpha[rb] = (live && m_run[rb] != -INFINITY) ? hx::fast_exp2((m_run[rb] - m_new) * sl2)
+                                                   : (live ? 0.f : 1.f);
       const float neg_m = live ? -m_new * sl2 : 0.f;
       float psum = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = exp2f(fmaf(sacc[kb][rb][i], sl2, neg_m));  // -inf -> 0
+          const float p = hx::fast_exp2(fmaf(sacc[kb][rb][i], sl2, neg_m));  // -inf -> 0
           sacc[kb][rb][i] = p;
           psum += p;
         }
@@ -835,14 +856,10 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
       m_run[rb] = m_new;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        uint16_t h8[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          h8[e] = E::bits(sacc[2 * ks][rb][e]);
-          h8[e + 4] = E::bits(sacc[2 * ks + 1][rb][e]);
-        }
-        const uint4 u = make_uint4(hx::pack2(h8[0], h8[1]), hx::pack2(h8[2], h8[3]),
-                                   hx::pack2(h8[4], h8[5]), hx::pack2(h8[6], h8[7]));
+        const hx::f32x4_t& x = sacc[2 * ks][rb];
+        const hx::f32x4_t& y = sacc[2 * ks + 1][rb];
+        const uint4 u = make_uint4(hx::pack2_round<T>(x[0], x[1]), hx::pack2_round<T>(x[2], x[3]),
+                                   hx::pack2_round<T>(y[0], y[1]), hx::pack2_round<T>(y[2], y[3]));
         pb[ks][rb] = hx::as_v8<T>(u);
       }
     }
@@ -884,8 +901,8 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
 #pragma unroll
       for (int db = 0; db < 8; ++db) {
         const int d0 = 16 * db + 4 * (lane >> 4);
-        const uint2 u = make_uint2(hx::pack2(E::bits(oacc[db][rb][0] * inv), E::bits(oacc[db][rb][1] * inv)),
-                                   hx::pack2(E::bits(oacc[db][rb][2] * inv), E::bits(oacc[db][rb][3] * inv)));
+        const uint2 u = make_uint2(hx::pack2_round<T>(oacc[db][rb][0] * inv, oacc[db][rb][1] * inv),
+                                   hx::pack2_round<T>(oacc[db][rb][2] * inv, oacc[db][rb][3] * inv));
         *reinterpret_cast<uint2*>(orow + d0) = u;
       }
       if (a.lse && (lane >> 4) == 0)
