@@ -257,7 +257,8 @@ def long_context(device, steps: int = 10, warmup: int = 3):
 
 
 def pmc_pass(device):
-    """Counter-collection run: a page copy of known size, then decode steps."""
+    """Counter-collection run: a page copy of known size, then decode-tick steps, then
+    mixed-tick and long-context steps (their chunk launches carry the MFMA counters)."""
     import torch
 
     from helios_amd import ops, synth
@@ -269,13 +270,27 @@ def pmc_pass(device):
         ops.kv_copy_pages(pools, None, src, dst)
     torch.cuda.synchronize()
     copy_bytes = layers * 64 * pools[0][0].numel() * 2
+    del pools
     b = DecodeBench(synth.c2(), device, copies=POOL_COPIES)
     for i in range(8):
         b.step(i % POOL_COPIES)
     torch.cuda.synchronize()
+    decode_bytes = b.w.decode_bytes()
+    del b
+    chunk_flops = {}
+    for name in ("c3", "c4"):
+        w = getattr(synth, name)()
+        b = DecodeBench(w, device, copies=1)
+        for _ in range(3):
+            b.step(0)
+        torch.cuda.synchronize()
+        chunk_flops[name] = w.chunk_flops()
+        del b
+        torch.cuda.empty_cache()
     print(json.dumps({"pmc_pass": True, "copy_read_bytes_per_dispatch": copy_bytes,
                       "copy_write_bytes_per_dispatch": copy_bytes,
-                      "decode_algorithmic_bytes": b.w.decode_bytes()}), flush=True)
+                      "decode_algorithmic_bytes": decode_bytes,
+                      "chunk_flops": chunk_flops}), flush=True)
 
 
 def main():

@@ -661,7 +661,9 @@ constexpr int kChunkThreads = 512;     // 8 waves: 2 per SIMD
 // One workgroup per (sequence, block of 256/Gw query rows, group of Gw <= 4 query
 // heads of KV head g). Wave w owns 32 rows (two 16-row MFMA blocks) of head w % Gw.
 // Each 64-key tile of K (row-major) and V (transposed, key pairs packed per 32-bit
-// word) goes through LDS once and feeds all 8 waves; the next tile is prefetched into
+// word; in V^T row d the key-pair column kp is stored at kp ^ 2*(d >> 4), which spreads
+// the transposing writes of one wave over all LDS banks and leaves the 16-row fragment
+// reads conflict-free) goes through LDS once and feeds all 8 waves; the next tile is prefetched into
 // registers while the current one is consumed. Two waves per SIMD hide each other's
 // LDS and memory latency.
 template <typename T, int G>
@@ -774,8 +776,9 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
     for (int j = 0; j < 2; ++j)
       *reinterpret_cast<uint4*>(&k_lds[(kr_base + 32 * j) * kKStride + 8 * c16]) = kreg[j];
     {
+      // Rows d = 8*c16 + 0..7 share the key-pair swizzle (d >> 4) = c16 >> 1.
       const uint4 x = vreg[0], y = vreg[1];
-      const int kp2 = 2 * kr_base;
+      const int kp2 = 2 * (kr_base ^ (c16 & 14));
       const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
       const uint32_t ys[4] = {y.x, y.y, y.z, y.w};
 #pragma unroll
@@ -877,9 +880,10 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
     for (int db = 0; db < 8; ++db) {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const T* vrow = &vt_lds[(16 * db + (lane & 15)) * kVStride + 32 * ks + 4 * (lane >> 4)];
-        const uint2 lo8 = *reinterpret_cast<const uint2*>(vrow);
-        const uint2 hi8 = *reinterpret_cast<const uint2*>(vrow + 16);
+        const T* vrow = &vt_lds[(16 * db + (lane & 15)) * kVStride];
+        const int kp = (16 * ks + 2 * (lane >> 4)) ^ (2 * db);  // swizzled key pair of keys 0..3
+        const uint2 lo8 = *reinterpret_cast<const uint2*>(vrow + 2 * kp);
+        const uint2 hi8 = *reinterpret_cast<const uint2*>(vrow + 2 * (kp ^ 8));
         const v8 af = hx::as_v8<T>(make_uint4(lo8.x, lo8.y, hi8.x, hi8.y));
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) oacc[db][rb] = E::mfma16x16x32(af, pb[ks][rb], oacc[db][rb]);
