@@ -655,17 +655,28 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(RunArgs a) {
 
 // ------------------------------------------------------------------ chunk (prefill) MFMA
 constexpr int kKStride = kD + 8;       // K tile row: 136 elements (272 B)
-constexpr int kVStride = kTile + 4;    // V^T tile row: 68 elements (136 B)
+constexpr int kVStride = kTile + 8;    // V^T tile row: 72 elements (144 B = 36 dwords)
 constexpr int kChunkThreads = 512;     // 8 waves: 2 per SIMD
+constexpr float kLazyLog2 = 8.f;       // softmax terms stay <= 2^8 between max updates
+
+// V^T tile layout. Row d holds the 64 keys of dim d as 32 dwords (key pairs) in eight
+// 16-byte groups. Group 4*ks + q holds, in this order, keys 32ks + 4q + 0..3 and
+// 32ks + 16 + 4q + 0..3: the eight k-values that lane (q, row) feeds to the PV MFMA,
+// so each operand is one ds_read_b128. Group gi of row d sits at gi ^ (d >> 4): the
+// 16 rows one fragment read touches share the XOR (conflict-free reads, rows 36 dwords
+// apart), and the 64 transposing writes of a wave (16 dim chunks x key pairs differing
+// in bits 0 and 3) land on distinct banks.
+__device__ __forceinline__ int vt_col(int kp, int dblk) {
+  const int p = kp & 15;
+  const int gi = 4 * (kp >> 4) + ((p & 7) >> 1);
+  return ((gi ^ dblk) << 2) | (2 * (p >> 3) + (p & 1));
+}
 
 // One workgroup per (sequence, block of 256/Gw query rows, group of Gw <= 4 query
 // heads of KV head g). Wave w owns 32 rows (two 16-row MFMA blocks) of head w % Gw.
-// Each 64-key tile of K (row-major) and V (transposed, key pairs packed per 32-bit
-// word; in V^T row d the key-pair column kp is stored at kp ^ 2*(d >> 4), which spreads
-// the transposing writes of one wave over all LDS banks and leaves the 16-row fragment
-// reads conflict-free) goes through LDS once and feeds all 8 waves; the next tile is prefetched into
-// registers while the current one is consumed. Two waves per SIMD hide each other's
-// LDS and memory latency.
+// Each 64-key tile of K (row-major) and V (transposed as above) goes through LDS once
+// and feeds all 8 waves; the next tile is prefetched into registers while the current
+// one is consumed. Two waves per SIMD hide each other's LDS and memory latency.
 template <typename T, int G>
 __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   typedef hx::Elem<T> E;
@@ -700,6 +711,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   const int wr0 = row0 + 32 * (w / Gw);
   const int qh = g * G + hquad * Gw + (w % Gw);
   const float sl2 = a.scale_log2;
+  const float lazy_thr = kLazyLog2 / sl2;  // raw-score margin before the reference max moves
 
   // Q^T as the MFMA B operand: lane holds row wr0+16rb+(lane&15), dims 32st+8(lane>>4)..+7.
   uint4 qf[2][4];
@@ -722,7 +734,12 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   float l_run[2] = {0.f, 0.f};              // this lane's share of the row sum
 
   const int c16 = tid & 15;     // 16-byte chunk of a key row this thread moves
-  const int kr_base = tid >> 4; // 0..31
+  const int kr_base = tid >> 4; // K rows kr_base and kr_base + 32
+  // V rows 2*vkp and 2*vkp + 1 (key pair vkp). Within a wave the four pairs differ in
+  // bits 0 and 3, so the transposing writes below reach all LDS banks.
+  const int vkp = ((tid >> 4) & 1) + 8 * ((tid >> 5) & 1) + 2 * ((tid >> 6) & 3) + 16 * (tid >> 8);
+  // Dword column of key pair vkp in V^T rows d = 8*c16 + 0..7 (see vt_col).
+  const int vcol = vt_col(vkp, c16 >> 1);
 
   // Page ids of the key range, 64 at a time: lane j holds the id of page pg_base + j,
   // so a tile finds its page with one v_readlane instead of a dependent global load.
@@ -765,7 +782,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       kreg[j] = ld16(kp + min(kr_base + 32 * j, kmax) * kvr);
-      vreg[j] = ld16(vp + min(2 * kr_base + j, kmax) * kvr);
+      vreg[j] = ld16(vp + min(2 * vkp + j, kmax) * kvr);
     }
   };
 
@@ -776,16 +793,15 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
     for (int j = 0; j < 2; ++j)
       *reinterpret_cast<uint4*>(&k_lds[(kr_base + 32 * j) * kKStride + 8 * c16]) = kreg[j];
     {
-      // Rows d = 8*c16 + 0..7 share the key-pair swizzle (d >> 4) = c16 >> 1.
       const uint4 x = vreg[0], y = vreg[1];
-      const int kp2 = 2 * (kr_base ^ (c16 & 14));
       const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
       const uint32_t ys[4] = {y.x, y.y, y.z, y.w};
+      uint32_t* vt32 = reinterpret_cast<uint32_t*>(vt_lds);
 #pragma unroll
       for (int wd = 0; wd < 4; ++wd) {
         const int d = 8 * c16 + 2 * wd;
-        *reinterpret_cast<uint32_t*>(&vt_lds[d * kVStride + kp2]) = hx::interleave_lo(xs[wd], ys[wd]);
-        *reinterpret_cast<uint32_t*>(&vt_lds[(d + 1) * kVStride + kp2]) = hx::interleave_hi(xs[wd], ys[wd]);
+        vt32[d * (kVStride / 2) + vcol] = hx::interleave_lo(xs[wd], ys[wd]);
+        vt32[(d + 1) * (kVStride / 2) + vcol] = hx::interleave_hi(xs[wd], ys[wd]);
       }
     }
     __syncthreads();
@@ -841,11 +857,15 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
         mx = fmaxf(mx, fmaxf(fmaxf(sacc[kb][rb][0], sacc[kb][rb][1]), fmaxf(sacc[kb][rb][2], sacc[kb][rb][3])));
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run[rb], mx);
-      const bool live = m_new != -INFINITY;
-      alpha[rb] = (live && m_run[rb] != -INFINITY) ? hx::fast_exp2((m_run[rb] - m_new) * sl2)
-                                                   : (live ? 0.f : 1.f);
-      const float neg_m = live ? -m_new * sl2 : 0.f;
+      // Lazy max: the row's reference max moves only when the tile max exceeds it by more
+      // than kLazyLog2 (log2 units). Until then p = 2^((s - m_run) * sl2) <= 2^kLazyLog2,
+      // which the fp32 sums and bf16 P carry as accurately as p <= 1. The first finite
+      // max sets it with alpha = 1, as l and O are still zero.
+      const bool first = m_run[rb] == -INFINITY;
+      const bool move = mx != -INFINITY && (first || mx > m_run[rb] + lazy_thr);
+      alpha[rb] = move && !first ? hx::fast_exp2((m_run[rb] - mx) * sl2) : 1.f;
+      const float m_new = move ? mx : m_run[rb];
+      const float neg_m = m_new != -INFINITY ? -m_new * sl2 : 0.f;
       float psum = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
@@ -866,8 +886,8 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
         pb[ks][rb] = hx::as_v8<T>(u);
       }
     }
-    // Rescale the accumulators only when some row's max moved (after the first tiles of
-    // a row this is rare).
+    // Rescale the accumulators only when some row's reference max moved (rare after a
+    // row's first tile).
     if (__any(alpha[0] != 1.f || alpha[1] != 1.f)) {
 #pragma unroll
       for (int db = 0; db < 8; ++db)
@@ -877,17 +897,17 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
 
     // O^T += V^T P^T with the key order of pb: {4(lane>>4)+0..3, 16+4(lane>>4)+0..3}.
 #pragma unroll
-    for (int db = 0; db < 8; ++db) {
+    for (int ks = 0; ks < 2; ++ks) {
+      uint4 vf[8];  // all eight dim blocks of this key step, read before their MFMAs
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const T* vrow = &vt_lds[(16 * db + (lane & 15)) * kVStride];
-        const int kp = (16 * ks + 2 * (lane >> 4)) ^ (2 * db);  // swizzled key pair of keys 0..3
-        const uint2 lo8 = *reinterpret_cast<const uint2*>(vrow + 2 * kp);
-        const uint2 hi8 = *reinterpret_cast<const uint2*>(vrow + 2 * (kp ^ 8));
-        const v8 af = hx::as_v8<T>(make_uint4(lo8.x, lo8.y, hi8.x, hi8.y));
+      for (int db = 0; db < 8; ++db)
+        vf[db] = *reinterpret_cast<const uint4*>(
+            &vt_lds[(16 * db + (lane & 15)) * kVStride + 8 * ((4 * ks + (lane >> 4)) ^ db)]);
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) oacc[db][rb] = E::mfma16x16x32(af, pb[ks][rb], oacc[db][rb]);
-      }
+      for (int db = 0; db < 8; ++db)
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+          oacc[db][rb] = E::mfma16x16x32(hx::as_v8<T>(vf[db]), pb[ks][rb], oacc[db][rb]);
     }
     __syncthreads();
   }
