@@ -2,8 +2,8 @@
 
 The library exports the C ABI declared in ``include/helios_paged.h``. It is built
 from the ``.hip`` sources under ``helios_amd/csrc`` for gfx950 only, with packed
-FP32 instructions disabled, and written next to this file so that it travels with
-the source tree.
+FP32 instructions disabled and device code in non-IEEE mode (no NaN operands are
+assumed), and written next to this file so that it travels with the source tree.
 """
 
 from __future__ import annotations
@@ -39,6 +39,9 @@ def compile_command(output: Path, *, resource_usage: bool = False) -> list[str]:
         "-fPIC",
         "-shared",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # Device code: no NaN operands are assumed and IEEE mode is off, so fmaxf on MFMA
+        # results needs no canonicalising pass per element.
+        "-Xarch_device", "-fno-honor-nans", "-Xarch_device", "-mno-amdgpu-ieee",
         f"-I{INCLUDE}",
         "-o", str(output),
     ]

@@ -685,7 +685,8 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   __shared__ __attribute__((aligned(16))) T k_lds[kTile * kKStride];
   __shared__ __attribute__((aligned(16))) T vt_lds[kD * kVStride];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, held in a scalar register
   const int item = (int)blockIdx.x / a.hkv;
   const int g = (int)blockIdx.x - item * a.hkv;
   const Header hd = read_header(a);
@@ -711,7 +712,8 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   const int wr0 = row0 + 32 * (w / Gw);
   const int qh = g * G + hquad * Gw + (w % Gw);
   const float sl2 = a.scale_log2;
-  const float lazy_thr = kLazyLog2 / sl2;  // raw-score margin before the reference max moves
+  // Raw-score margin before the reference max moves (finite, so -inf + margin = -inf).
+  const float lazy_thr = fminf(kLazyLog2 / sl2, 1e30f);
 
   // Q^T as the MFMA B operand: lane holds row wr0+16rb+(lane&15), dims 32st+8(lane>>4)..+7.
   uint4 qf[2][4];
@@ -826,29 +828,32 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
       }
     }
 
-    // Mask only where the tile is not fully visible to every row of this wave.
-    bool full = (n - wr0 >= 32) && (t0 + kTile - 1 <= L - 1);
-    if (a.win_left >= 0) full = full && (off + wr0 + 31 - a.win_left <= t0);
-    if (a.win_right >= 0) full = full && (off + wr0 + a.win_right >= t0 + kTile - 1);
+    // Mask only where the tile is not fully visible to every row of this wave (a
+    // wave-uniform test, evaluated on the scalar unit).
+    int full_i = (n - wr0 >= 32) & (t0 + kTile - 1 <= L - 1);
+    full_i &= (a.win_left < 0) | (off + wr0 + 31 - a.win_left <= t0);
+    full_i &= (a.win_right < 0) | (off + wr0 + a.win_right >= t0 + kTile - 1);
+    const bool full = __builtin_amdgcn_readfirstlane(full_i) != 0;
 
     v8 pb[2][2];
     float alpha[2];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-      const int rr = wr0 + 16 * rb + (lane & 15);
       if (!full) {
+        // Visible keys of this lane's row, relative to the lane's first key in the tile,
+        // so each element compares its compile-time offset 16*kb + i.
+        const int rr = wr0 + 16 * rb + (lane & 15);
         const int qpos = off + rr;
-        const int rlo = a.win_left >= 0 ? qpos - a.win_left : -2147483647;
+        const int kbase = t0 + 4 * (lane >> 4);
+        const int rlo = a.win_left >= 0 ? qpos - a.win_left - kbase : -kTile;
         int rhi = L - 1;
         if (a.win_right >= 0) rhi = min(rhi, qpos + a.win_right);
-        if (rr >= n) rhi = -1;
+        rhi = rr < n ? rhi - kbase : -1;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = t0 + 16 * kb + 4 * (lane >> 4) + i;
-            if (key < rlo || key > rhi) sacc[kb][rb][i] = -INFINITY;
-          }
+          for (int i = 0; i < 4; ++i)
+            if (16 * kb + i < rlo || 16 * kb + i > rhi) sacc[kb][rb][i] = -INFINITY;
       }
       // Row max on raw scores (the scale is positive), folded into exp2 by one FMA.
       float mx = fmaxf(fmaxf(sacc[0][rb][0], sacc[0][rb][1]), fmaxf(sacc[0][rb][2], sacc[0][rb][3]));
@@ -859,11 +864,11 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       // Lazy max: the row's reference max moves only when the tile max exceeds it by more
       // than kLazyLog2 (log2 units). Until then p = 2^((s - m_run) * sl2) <= 2^kLazyLog2,
-      // which the fp32 sums and bf16 P carry as accurately as p <= 1. The first finite
-      // max sets it with alpha = 1, as l and O are still zero.
-      const bool first = m_run[rb] == -INFINITY;
-      const bool move = mx != -INFINITY && (first || mx > m_run[rb] + lazy_thr);
-      alpha[rb] = move && !first ? hx::fast_exp2((m_run[rb] - mx) * sl2) : 1.f;
+      // which the fp32 sums and bf16 P carry as accurately as p <= 1. With m_run = -inf
+      // the test is mx > -inf (the first finite max sets it; alpha = 2^-inf = 0 then
+      // multiplies the still-zero l and O); an all-masked tile (mx = -inf) never moves it.
+      const bool move = mx > m_run[rb] + lazy_thr;
+      alpha[rb] = move ? hx::fast_exp2((m_run[rb] - mx) * sl2) : 1.f;
       const float m_new = move ? mx : m_run[rb];
       const float neg_m = m_new != -INFINITY ? -m_new * sl2 : 0.f;
       float psum = 0.f;
