@@ -695,10 +695,15 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   const int n_pf = hd.counts.y;
   if (blockIdx.x == 0 && tid == 0 && n_pf > a.grid_pf) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
   if (item >= n_pf) return;
-  const int b = it.x, row0 = it.y, hquad = it.z;
+  // Work-item and sequence fields are workgroup-uniform: keep them (and the tile loop
+  // they bound) in scalar registers.
+  const int b = __builtin_amdgcn_readfirstlane(it.x);
+  const int row0 = __builtin_amdgcn_readfirstlane(it.y);
+  const int hquad = __builtin_amdgcn_readfirstlane(it.z);
   if ((unsigned)b >= (unsigned)a.batch) return;
   const int4 si = a.seq_info[b];
-  const int q0 = si.x, n = si.y, L = si.z, kvb = si.w;
+  const int q0 = __builtin_amdgcn_readfirstlane(si.x), n = __builtin_amdgcn_readfirstlane(si.y);
+  const int L = __builtin_amdgcn_readfirstlane(si.z), kvb = __builtin_amdgcn_readfirstlane(si.w);
   const int off = L - n;  // key position of query row 0
   const int wg_row_end = min(n, row0 + 32 * (8 / Gw));
 
@@ -754,6 +759,15 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
     pg_ids = p <= last_pg ? a.bt[(int64_t)b * a.bt_stride + p] : -1;
   };
   if (paged) fetch_pages();
+  // Tiles are loaded in key order; (ld_pi, ld_off) = page index and in-page key offset of
+  // the next tile to load (pages hold a whole number of tiles).
+  int ld_pi = pg_base, ld_off = paged ? t_begin * kTile - pg_base * a.page_size : 0;
+
+  // Per-thread element offsets of the rows this thread loads, relative to the tile's first
+  // row of KV head g.
+  const int kvr = (int)a.kv_row;
+  const int koff0 = kr_base * kvr + 8 * c16, koff1 = koff0 + 32 * kvr;
+  const int voff0 = 2 * vkp * kvr + 8 * c16, voff1 = voff0 + kvr;
 
   // Key rows past L - 1 (only in the last tile) load row L - 1 instead, which lies in the
   // same page; their scores are masked to -inf, so no branch guards the loads. A bad page
@@ -761,30 +775,40 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   uint4 kreg[2], vreg[2];
   auto load_tile = [&](int t) {
     const int key_base = t * kTile;
-    const int kmax = min(L - 1 - key_base, kTile - 1);  // >= 0: key_base <= khi <= L - 1
     int64_t rowb;
     if (paged) {
-      const int pi = key_base / a.page_size;
-      if (pi - pg_base >= 64) {
-        pg_base = pi;
+      if (ld_pi - pg_base >= 64) {
+        pg_base = ld_pi;
         fetch_pages();
       }
-      int page = __builtin_amdgcn_readlane(pg_ids, pi - pg_base);
+      int page = __builtin_amdgcn_readlane(pg_ids, ld_pi - pg_base);
       if ((unsigned)page >= (unsigned)a.num_pages) {
         if (tid == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_BAD_PAGE);
         page = 0;
       }
-      rowb = (int64_t)page * a.page_size + (key_base - pi * a.page_size);
+      rowb = (int64_t)page * a.page_size + ld_off;
+      ld_off += kTile;
+      if (ld_off == a.page_size) {
+        ld_off = 0;
+        ++ld_pi;
+      }
     } else {
       rowb = (int64_t)kvb + key_base;
     }
-    const T* kp = reinterpret_cast<const T*>(a.k) + rowb * a.kv_row + (int64_t)g * a.kv_head + 8 * c16;
-    const T* vp = reinterpret_cast<const T*>(a.v) + rowb * a.kv_row + (int64_t)g * a.kv_head + 8 * c16;
-    const int kvr = (int)a.kv_row;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      kreg[j] = ld16(kp + min(kr_base + 32 * j, kmax) * kvr);
-      vreg[j] = ld16(vp + min(2 * vkp + j, kmax) * kvr);
+    const int64_t head0 = rowb * a.kv_row + (int64_t)g * a.kv_head;
+    const T* kt = reinterpret_cast<const T*>(a.k) + head0;
+    const T* vt = reinterpret_cast<const T*>(a.v) + head0;
+    const int kmax = L - 1 - key_base;  // >= 0: key_base <= khi <= L - 1
+    if (kmax >= kTile - 1) {
+      kreg[0] = ld16(kt + koff0);
+      kreg[1] = ld16(kt + koff1);
+      vreg[0] = ld16(vt + voff0);
+      vreg[1] = ld16(vt + voff1);
+    } else {
+      kreg[0] = ld16(kt + min(kr_base, kmax) * kvr + 8 * c16);
+      kreg[1] = ld16(kt + min(kr_base + 32, kmax) * kvr + 8 * c16);
+      vreg[0] = ld16(vt + min(2 * vkp, kmax) * kvr + 8 * c16);
+      vreg[1] = ld16(vt + min(2 * vkp + 1, kmax) * kvr + 8 * c16);
     }
   };
 
