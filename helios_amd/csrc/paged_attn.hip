@@ -384,7 +384,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
   __shared__ float fin_m[8];
   __shared__ float fin_l[8];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, held in a scalar register
   const int item = (int)blockIdx.x / a.hkv;
   const int g = (int)blockIdx.x - item * a.hkv;
   // The work item is read together with the header (item < grid_dec <= the list's
@@ -395,7 +396,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
   const int n_dec = hd.counts.x;
   if (blockIdx.x == 0 && tid == 0 && n_dec > a.grid_dec) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
   if (item >= n_dec) return;
-  const int b = it.x, s = it.y, q0 = it.z, L = it.w;
+  // Workgroup-uniform: kept in scalar registers.
+  const int b = __builtin_amdgcn_readfirstlane(it.x), s = __builtin_amdgcn_readfirstlane(it.y);
+  const int q0 = __builtin_amdgcn_readfirstlane(it.z), L = __builtin_amdgcn_readfirstlane(it.w);
   if ((unsigned)b >= (unsigned)a.batch) return;
   int s_first, splits;
   decode_splits(L, a.win_left, &s_first, &splits);
