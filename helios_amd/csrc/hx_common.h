@@ -79,6 +79,14 @@ __device__ __forceinline__ uint32_t pack2_round<_Float16>(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, h2));
 }
 
+// Eight packed 1.0 values of element type T.
+template <typename T>
+__device__ __forceinline__ uint4 ones8();
+template <>
+__device__ __forceinline__ uint4 ones8<__bf16>() { return make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u); }
+template <>
+__device__ __forceinline__ uint4 ones8<_Float16>() { return make_uint4(0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u); }
+
 template <typename T>
 __device__ __forceinline__ typename Elem<T>::v8 as_v8(uint4 u) {
   return __builtin_bit_cast(typename Elem<T>::v8, u);

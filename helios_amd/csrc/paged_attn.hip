@@ -898,25 +898,25 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
       alpha[rb] = move ? hx::fast_exp2((m_run[rb] - mx) * sl2) : 1.f;
       const float m_new = move ? mx : m_run[rb];
       const float neg_m = m_new != -INFINITY ? -m_new * sl2 : 0.f;
-      float psum = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = hx::fast_exp2(fmaf(sacc[kb][rb][i], sl2, neg_m));  // -inf -> 0
-          sacc[kb][rb][i] = p;
-          psum += p;
-        }
-      l_run[rb] = l_run[rb] * alpha[rb] + psum;
-      m_run[rb] = m_new;
+        for (int i = 0; i < 4; ++i)
+          sacc[kb][rb][i] = hx::fast_exp2(fmaf(sacc[kb][rb][i], sl2, neg_m));  // -inf -> 0
+      // P in the MFMA's element type; the row sum adds the same rounded values (two per
+      // dot2 against {1, 1}), so l matches the weights applied to V exactly.
+      float psum = 0.f;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const hx::f32x4_t& x = sacc[2 * ks][rb];
         const hx::f32x4_t& y = sacc[2 * ks + 1][rb];
         const uint4 u = make_uint4(hx::pack2_round<T>(x[0], x[1]), hx::pack2_round<T>(x[2], x[3]),
                                    hx::pack2_round<T>(y[0], y[1]), hx::pack2_round<T>(y[2], y[3]));
+        psum = hx::dot8<T>(u, hx::ones8<T>(), psum);
         pb[ks][rb] = hx::as_v8<T>(u);
       }
+      l_run[rb] = l_run[rb] * alpha[rb] + psum;
+      m_run[rb] = m_new;
     }
     // Rescale the accumulators only when some row's reference max moved (rare after a
     // row's first tile).
