@@ -108,6 +108,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_void_p, _size, _c_void_p],
     ),
     "hx_varlen_attn_error_word_offset": (_size, []),
+    "hx_tick_metadata": (
+        ctypes.c_int,
+        [_c_void_p, _i32, _i32, _i32,
+         _c_void_p, _i32, _i32,
+         _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p],
+    ),
 }
 
 _lib: ctypes.CDLL | None = None

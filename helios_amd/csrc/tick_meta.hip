@@ -1,0 +1,156 @@
+// Per-tick attention metadata built on the device (gfx950).
+//
+// Reference: PagedBatchCache.prepare (src/helios/runtime/qwen3/paged_cache.py:221-270)
+// and PackedBatchCache.prepare_packed (:418-494) build cu_seq_q, cu_seq_k, seqused_k,
+// positions, logit_indices and write_slots as Python lists, one entry per token, and
+// copy each to the device through `metadata` (:272-288). Here the host uploads three
+// int32 values per sequence (length before the tick, tokens this tick, logit rows) and
+// one launch derives every array: workgroup 0 writes the per-sequence arrays and the
+// logit indices, workgroups 1.. write one token row per thread.
+
+#include "hx_common.h"
+
+namespace {
+
+constexpr int kMetaThreads = 256;
+constexpr int kMetaMaxBatch = 4096;
+
+struct MetaArgs {
+  const int32_t* seq;  // lengths[B], counts[B], logit_counts[B]
+  int32_t batch;
+  int32_t total_q;
+  int32_t n_logits;
+  const int32_t* bt;
+  int32_t bt_stride;
+  int32_t page_size;
+  int32_t* cu_q;
+  int32_t* cu_k;
+  int32_t* used_k;
+  int64_t* positions;
+  int64_t* slots;
+  int64_t* logit_idx;
+};
+
+// Exclusive prefix sum of in[0..n) into out[0..n] (out[n] = total) by one workgroup.
+// Each thread sums a contiguous run of ceil(n / 256) values; the 256 run totals are
+// scanned in LDS (Hillis-Steele); then each thread writes its run.
+__device__ void block_scan(const int32_t* in, int32_t* out, int n, int32_t* part) {
+  const int tid = threadIdx.x;
+  const int per = (n + kMetaThreads - 1) / kMetaThreads;
+  const int lo = min(n, tid * per), hi = min(n, lo + per);
+  int32_t run = 0;
+  for (int i = lo; i < hi; ++i) run += in[i];
+  part[tid] = run;
+  __syncthreads();
+  for (int d = 1; d < kMetaThreads; d <<= 1) {
+    const int32_t add = tid >= d ? part[tid - d] : 0;
+    __syncthreads();
+    part[tid] += add;
+    __syncthreads();
+  }
+  int32_t acc = part[tid] - run;  // exclusive prefix of this run
+  for (int i = lo; i < hi; ++i) {
+    out[i] = acc;
+    acc += in[i];
+  }
+  if (tid == kMetaThreads - 1) out[n] = part[tid];
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(kMetaThreads) void tick_meta_kernel(MetaArgs a) {
+  __shared__ int32_t s_len[kMetaMaxBatch];
+  __shared__ int32_t s_cnt[kMetaMaxBatch];
+  __shared__ int32_t s_cuq[kMetaMaxBatch + 1];
+  __shared__ int32_t s_aux[kMetaMaxBatch + 1];
+  __shared__ int32_t s_part[kMetaThreads];
+  const int B = a.batch, tid = threadIdx.x;
+  for (int b = tid; b < B; b += kMetaThreads) {
+    s_len[b] = a.seq[b];
+    s_cnt[b] = a.seq[B + b];
+  }
+  __syncthreads();
+  block_scan(s_cnt, s_cuq, B, s_part);
+
+  if (blockIdx.x == 0) {
+    for (int b = tid; b <= B; b += kMetaThreads) a.cu_q[b] = s_cuq[b];
+    // Sequence ends E_b = length + count, their prefix sums, and seqused_k.
+    for (int b = tid; b < B; b += kMetaThreads) {
+      const int32_t e = s_len[b] + s_cnt[b];
+      a.used_k[b] = e;
+      s_len[b] = e;  // s_len now holds the ends
+    }
+    __syncthreads();
+    block_scan(s_len, s_aux, B, s_part);
+    for (int b = tid; b <= B; b += kMetaThreads) a.cu_k[b] = s_aux[b];
+    if (a.logit_idx != nullptr) {
+      __syncthreads();
+      for (int b = tid; b < B; b += kMetaThreads) s_len[b] = a.seq[2 * B + b];  // logit rows
+      __syncthreads();
+      block_scan(s_len, s_aux, B, s_part);
+      for (int b = tid; b < B; b += kMetaThreads) {
+        const int tail = s_len[b];
+        const int end = s_cuq[b + 1];
+        for (int i = 0; i < tail; ++i) {
+          const int o = s_aux[b] + i;
+          if (o < a.n_logits) a.logit_idx[o] = (int64_t)(end - tail + i);
+        }
+      }
+    }
+    return;
+  }
+
+  // Token rows: row t belongs to the last sequence b with cu_q[b] <= t.
+  const int t = (int)(blockIdx.x - 1) * kMetaThreads + tid;
+  if (t >= a.total_q) return;
+  int64_t pos = -1, slot = -1;
+  if (t < s_cuq[B]) {
+    int lo = 0, hi = B - 1;  // invariant: s_cuq[lo] <= t < s_cuq[hi + 1]
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_cuq[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    const int b = lo;
+    pos = (int64_t)s_len[b] + (t - s_cuq[b]);
+    const int64_t pi = pos / a.page_size;
+    if (pi < a.bt_stride) {
+      const int32_t page = a.bt[(int64_t)b * a.bt_stride + pi];
+      slot = (int64_t)page * a.page_size + (pos - pi * a.page_size);
+    }
+  }
+  if (a.positions != nullptr) a.positions[t] = pos;
+  a.slots[t] = slot;
+}
+
+}  // namespace
+
+extern "C" int hx_tick_metadata(const int32_t* seq, int32_t batch, int32_t total_q,
+                                int32_t n_logits, const int32_t* block_table,
+                                int32_t block_table_stride, int32_t page_size,
+                                int32_t* cu_seq_q, int32_t* cu_seq_k, int32_t* seqused_k,
+                                int64_t* positions, int64_t* write_slots,
+                                int64_t* logit_indices, void* stream) {
+  if (batch < 1 || batch > kMetaMaxBatch || total_q < 0 || n_logits < 0 || page_size < 1 ||
+      block_table_stride < 1)
+    return HX_E_INVALID_ARG;
+  if (!seq || !block_table || !cu_seq_q || !cu_seq_k || !seqused_k || !write_slots)
+    return HX_E_INVALID_ARG;
+  if (n_logits > 0 && !logit_indices) return HX_E_INVALID_ARG;
+  MetaArgs a;
+  a.seq = seq;
+  a.batch = batch;
+  a.total_q = total_q;
+  a.n_logits = n_logits;
+  a.bt = block_table;
+  a.bt_stride = block_table_stride;
+  a.page_size = page_size;
+  a.cu_q = cu_seq_q;
+  a.cu_k = cu_seq_k;
+  a.used_k = seqused_k;
+  a.positions = positions;
+  a.slots = write_slots;
+  a.logit_idx = n_logits > 0 ? logit_indices : nullptr;
+  const unsigned grid = 1u + (unsigned)((total_q + kMetaThreads - 1) / kMetaThreads);
+  hipLaunchKernelGGL(tick_meta_kernel, dim3(grid), dim3(kMetaThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), a);
+  return hx::status_from_hip(hipGetLastError());
+}

@@ -105,6 +105,61 @@ def _check_append(k_cache, v_cache, write_slots, keys, values) -> None:
         raise ValueError("Appended K/V must have a contiguous head_dim.")
 
 
+# --------------------------------------------------------------- tick metadata
+def tick_metadata(
+    seq: torch.Tensor,
+    block_table: torch.Tensor,
+    page_size: int,
+    *,
+    total_q: int,
+    cu_seq_q: torch.Tensor,
+    cu_seq_k: torch.Tensor,
+    seqused_k: torch.Tensor,
+    write_slots: torch.Tensor,
+    positions: torch.Tensor | None = None,
+    logit_indices: torch.Tensor | None = None,
+    n_logits: int = 0,
+) -> None:
+    """Per-tick metadata of ``PagedBatchCache.prepare`` / ``PackedBatchCache.prepare_packed``
+    (paged_cache.py:221-270, :418-494) computed on the device.
+
+    ``seq``: int32 ``[3 * B]`` = lengths before the tick, tokens this tick, logit rows.
+    Writes ``cu_seq_q`` / ``cu_seq_k`` (int32 ``[B+1]``), ``seqused_k`` (int32 ``[B]``),
+    ``write_slots`` and optionally ``positions`` (int64, ``total_q`` rows) and
+    ``logit_indices`` (int64, ``n_logits`` rows), all preallocated on the device.
+    """
+    device = _require_gpu(seq, block_table, cu_seq_q, cu_seq_k, seqused_k, write_slots)
+    batch = seq.numel() // 3
+    if seq.dtype != torch.int32 or seq.numel() != 3 * batch or batch < 1 or not seq.is_contiguous():
+        raise ValueError("seq must be a contiguous int32 tensor of 3 * batch values.")
+    if block_table.dtype != torch.int32 or block_table.ndim != 2 or block_table.shape[0] != batch:
+        raise ValueError("block_table must be int32 [batch, width].")
+    if block_table.stride(1) != 1:
+        raise ValueError("block_table rows must be contiguous.")
+    for name, t, n, dt in (("cu_seq_q", cu_seq_q, batch + 1, torch.int32),
+                           ("cu_seq_k", cu_seq_k, batch + 1, torch.int32),
+                           ("seqused_k", seqused_k, batch, torch.int32),
+                           ("write_slots", write_slots, total_q, torch.int64)):
+        if t.dtype != dt or t.numel() < n or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous {dt} tensor of at least {n} values.")
+    for name, t, n in (("positions", positions, total_q), ("logit_indices", logit_indices, n_logits)):
+        if t is not None and (t.dtype != torch.int64 or t.numel() < n or not t.is_contiguous()
+                              or t.device != device):
+            raise ValueError(f"{name} must be a contiguous int64 tensor of at least {n} values.")
+    if n_logits > 0 and logit_indices is None:
+        raise ValueError("logit_indices is required when n_logits > 0.")
+    code = _capi.lib().hx_tick_metadata(
+        seq.data_ptr(), batch, total_q, n_logits,
+        block_table.data_ptr(), block_table.stride(0), page_size,
+        cu_seq_q.data_ptr(), cu_seq_k.data_ptr(), seqused_k.data_ptr(),
+        positions.data_ptr() if positions is not None else None,
+        write_slots.data_ptr(),
+        logit_indices.data_ptr() if logit_indices is not None else None,
+        _stream_ptr(device),
+    )
+    _capi.check(code, "hx_tick_metadata")
+
+
 # --------------------------------------------------------------------- page copy
 def kv_copy_pages(
     k_caches: Sequence[torch.Tensor],

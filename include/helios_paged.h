@@ -227,6 +227,36 @@ int hx_varlen_attn(const void* q, int64_t q_row_stride, int64_t q_head_stride,
  * cleared by each hx_varlen_attn_plan). */
 size_t hx_varlen_attn_error_word_offset(void);
 
+/*
+ * Tick metadata on the device. Replaces the per-token list building of
+ * PagedBatchCache.prepare (paged_cache.py:221-270) and PackedBatchCache.prepare_packed
+ * (:418-494), and the host-to-device copies of `metadata` (:272-288).
+ *
+ * `seq` is a DEVICE int32 array of 3*batch values: lengths[b] (tokens cached before the
+ * tick), counts[b] (tokens appended this tick) and logit_counts[b] (trailing rows of b
+ * that produce logits). With E_b = lengths[b] + counts[b]:
+ *   cu_seq_q  = [0, cumsum(counts)]          int32 [batch + 1]
+ *   cu_seq_k  = [0, cumsum(E)]               int32 [batch + 1]
+ *   seqused_k = E                            int32 [batch]
+ * and for packed row t = cu_seq_q[b] + i, i < counts[b], pos = lengths[b] + i:
+ *   positions[t]   = pos                                                       int64
+ *   write_slots[t] = block_table[b * stride + pos / page_size] * page_size
+ *                    + pos % page_size                                         int64
+ *   logit_indices  = for b in order: cu_seq_q[b+1] - logit_counts[b] .. cu_seq_q[b+1] - 1
+ * positions may be NULL, and logit_indices when n_logits == 0.
+ *
+ * total_q must be sum(counts) and n_logits must be sum(logit_counts). A row whose page
+ * index reaches block_table_stride gets write slot -1, which hx_kv_append skips (rows
+ * beyond sum(counts), if total_q is larger, get position -1 and slot -1). batch is at
+ * most 4096.
+ */
+int hx_tick_metadata(const int32_t* seq, int32_t batch, int32_t total_q, int32_t n_logits,
+                     const int32_t* block_table, int32_t block_table_stride,
+                     int32_t page_size,
+                     int32_t* cu_seq_q, int32_t* cu_seq_k, int32_t* seqused_k,
+                     int64_t* positions, int64_t* write_slots, int64_t* logit_indices,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif
