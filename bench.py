@@ -23,6 +23,8 @@ Printed JSON (one line):
             work only; the model's GEMMs are not part of this path).
   long_context  the long-context tick (8 x 32768 keys with a shared 16-page prefix +
             a 4096-token chunk) and the 36-layer restore copy of 16 prefix pages.
+  tick_metadata  host time of PackedBatchCache.prepare_packed with the reference's
+            per-token lists and copies vs the metadata kernel, and the kernel's time.
   cpu_baseline  the reference's dense-KV path (gather, repeat_interleave, SDPA) in
             torch fp32 on the host cores, on one full decode layer of the same tick.
 """
@@ -256,6 +258,67 @@ def long_context(device, steps: int = 10, warmup: int = 3):
     }
 
 
+def tick_metadata_leg(device, ticks: int = 20):
+    """Per-tick metadata of PackedBatchCache.prepare_packed: the reference's host lists
+    and pageable copies vs the metadata kernel, on the mixed tick (32 decoders + chunks
+    of 1024 and 992) and on a 128-decoder + 1024-chunk tick (the full-model shape).
+    Host time per prepare_packed call (what the scheduler thread waits for) and the
+    kernel's own time."""
+    import numpy as np
+    import torch
+
+    from helios_amd.config import Qwen3Config
+    from helios_amd.paged_cache import KVPagePool, PackedBatchCache, PagedKVCache
+
+    config = Qwen3Config(n_layers=1)
+    rng = np.random.default_rng(7)
+    shapes = {
+        "c3_mixed_tick": ([int(x) for x in rng.integers(1023, 4096, 32)] + [0, 512], [1] * 32 + [1024, 992]),
+        "decoders128_chunk1024": ([int(x) for x in rng.integers(1023, 8192, 128)] + [0], [1] * 128 + [1024]),
+    }
+    out = {}
+    for name, (lengths, counts) in shapes.items():
+        res = {"sequences": len(counts), "tokens": sum(counts)}
+        for mode in ("host_lists", "device_kernel"):
+            pages = sum(-(-(n + c * (ticks + 2)) // 256) for n, c in zip(lengths, counts)) + 8
+            pool = KVPagePool(config, pages, device=device)
+            caches = []
+            for n in lengths:
+                cache = PagedKVCache(pool, config.context_length)
+                cache.pages.extend(pool.acquire(-(-n // 256)))
+                cache.length = n
+                caches.append(cache)
+            batch = PackedBatchCache(caches, device_metadata=mode == "device_kernel")
+            times = []
+            for i in range(ticks + 2):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                batch.prepare_packed(counts)
+                t1 = time.perf_counter()
+                batch.advance_packed()
+                if i >= 2:
+                    times.append(t1 - t0)
+            torch.cuda.synchronize()
+            res[f"{mode}_us"] = round(statistics.median(times) * 1e6, 1)
+            if mode == "device_kernel":
+                ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+                meta = batch._device_meta
+                ev[0].record()
+                from helios_amd import ops
+                ops.tick_metadata(meta.seq, meta.block_table, 256, total_q=sum(counts),
+                                  cu_seq_q=meta.cu_seq_q, cu_seq_k=meta.cu_seq_k,
+                                  seqused_k=meta.seqused_k, write_slots=meta.write_slots,
+                                  positions=meta.positions, logit_indices=meta.logit_indices,
+                                  n_logits=len(counts))
+                ev[1].record()
+                torch.cuda.synchronize()
+                res["kernel_us"] = round(ev[0].elapsed_time(ev[1]) * 1e3, 2)
+            del batch, caches, pool
+            torch.cuda.empty_cache()
+        out[name] = res
+    return out
+
+
 def pmc_pass(device):
     """Counter-collection run: a page copy of known size, then decode-tick steps, then
     mixed-tick and long-context steps (their chunk launches carry the MFMA counters)."""
@@ -386,6 +449,7 @@ def main():
     if not args.no_packed_tick:
         result["packed_tick"] = packed_tick(device)
         result["long_context"] = long_context(device)
+        result["tick_metadata"] = tick_metadata_leg(device)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)
