@@ -108,6 +108,20 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_void_p, _size, _c_void_p],
     ),
     "hx_varlen_attn_error_word_offset": (_size, []),
+    "hx_qk_norm_rope_append": (
+        ctypes.c_int,
+        [_c_void_p, _i64, _i64,
+         _c_void_p, _i64, _i64,
+         _c_void_p, _i64, _i64,
+         _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p, _i64,
+         _c_void_p, _i64,
+         _i32, _i32, _i32,
+         _f32, _i32,
+         _c_void_p, _i64, _i64,
+         _c_void_p, _c_void_p, _i64,
+         _c_void_p, _c_void_p],
+    ),
     "hx_tick_metadata": (
         ctypes.c_int,
         [_c_void_p, _i32, _i32, _i32,

@@ -1,0 +1,154 @@
+// Per-head RMSNorm + RoPE of the new queries and keys, fused with the KV append (gfx950).
+//
+// Reference: GroupedQueryAttention.forward (src/helios/runtime/qwen3/layers.py:131-164)
+// applies q_norm / k_norm (RMSNorm over head_dim in fp32, layers.py:30-40), then
+// apply_rope (layers.py:54-72: x * cos + cat(-x2, x1) * sin in fp32, cast back), then
+// PagedBatchCache.attend appends K and V into the pool (_write, paged_cache.py:335-345).
+// Here one launch reads the projections once: queries come out normalised and rotated,
+// keys are normalised, rotated and stored straight into their pool rows, and values are
+// copied into theirs; the rotated keys never make a round trip through HBM.
+//
+// One wave per (row, head); lane l owns dims l and l + 64, which are exactly the pair
+// that RoPE mixes. The arithmetic follows the reference's op order with no fused
+// multiply-adds: n = bf16((x * rsqrt(mean(x^2) + eps)) * w), then
+// out = bf16(n * cos + (-n') * sin).
+
+#include "hx_common.h"
+
+namespace {
+
+constexpr int kRopeD = 128;
+constexpr int kRopeThreads = 256;
+
+struct RopeArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t q_row, q_head, k_row, k_head, v_row, v_head;
+  const float* q_scale;
+  const float* k_scale;
+  const float* cos;
+  const float* sin;
+  int64_t rope_rows;
+  const int64_t* positions;
+  int64_t n_rows;
+  int32_t hq, hkv;
+  float eps;
+  uint16_t* q_out;
+  int64_t qo_row, qo_head;
+  uint16_t* k_pool;
+  uint16_t* v_pool;
+  int64_t pool_rows;
+  const int64_t* slots;
+};
+
+template <typename T>
+__device__ __forceinline__ float to_f(uint16_t b) {
+  return (float)__builtin_bit_cast(T, b);
+}
+template <typename T>
+__device__ __forceinline__ uint16_t from_f(float f) {
+  return __builtin_bit_cast(uint16_t, (T)f);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_append_kernel(RopeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int heads = a.hq + 2 * a.hkv;
+  const int64_t items = a.n_rows * heads;
+  const int64_t step = (int64_t)gridDim.x * (kRopeThreads / 64);
+  for (int64_t it = (int64_t)blockIdx.x * (kRopeThreads / 64) + wave; it < items; it += step) {
+    const int64_t row = it / heads;
+    const int h = (int)(it - row * heads);
+    const int64_t slot = a.slots[row];
+    const bool slot_ok = slot >= 0 && slot < a.pool_rows;
+    if (h >= a.hq + a.hkv) {  // value head: plain copy into the pool
+      if (!slot_ok) continue;
+      const int hv = h - a.hq - a.hkv;
+      const uint16_t* src = a.v + row * a.v_row + hv * a.v_head;
+      uint16_t* dst = a.v_pool + (slot * a.hkv + hv) * kRopeD;
+      dst[lane] = src[lane];
+      dst[lane + 64] = src[lane + 64];
+      continue;
+    }
+    const bool is_q = h < a.hq;
+    const int hh = is_q ? h : h - a.hq;
+    if (!is_q && !slot_ok) continue;
+    const uint16_t* src = is_q ? a.q + row * a.q_row + hh * a.q_head : a.k + row * a.k_row + hh * a.k_head;
+    const float x0 = to_f<T>(src[lane]), x1 = to_f<T>(src[lane + 64]);
+    float ss = __fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1));
+    for (int m = 32; m >= 1; m >>= 1) ss = __fadd_rn(ss, __shfl_xor(ss, m));
+    const float r = rsqrtf(__fadd_rn(__fdiv_rn(ss, (float)kRopeD), a.eps));
+    const float* w = is_q ? a.q_scale : a.k_scale;
+    const float n0 = to_f<T>(from_f<T>(__fmul_rn(__fmul_rn(x0, r), w[lane])));
+    const float n1 = to_f<T>(from_f<T>(__fmul_rn(__fmul_rn(x1, r), w[lane + 64])));
+    int64_t pos = a.positions[row];
+    pos = pos < 0 ? 0 : (pos >= a.rope_rows ? a.rope_rows - 1 : pos);
+    const float* c = a.cos + pos * kRopeD;
+    const float* s = a.sin + pos * kRopeD;
+    const float o0 = __fadd_rn(__fmul_rn(n0, c[lane]), __fmul_rn(-n1, s[lane]));
+    const float o1 = __fadd_rn(__fmul_rn(n1, c[lane + 64]), __fmul_rn(n0, s[lane + 64]));
+    uint16_t* dst = is_q ? a.q_out + row * a.qo_row + hh * a.qo_head
+                         : a.k_pool + (slot * a.hkv + hh) * kRopeD;
+    dst[lane] = from_f<T>(o0);
+    dst[lane + 64] = from_f<T>(o1);
+  }
+}
+
+}  // namespace
+
+extern "C" int hx_qk_norm_rope_append(
+    const void* q, int64_t q_row_stride, int64_t q_head_stride,
+    const void* k, int64_t k_row_stride, int64_t k_head_stride,
+    const void* v, int64_t v_row_stride, int64_t v_head_stride,
+    const float* q_norm_weight, const float* k_norm_weight,
+    const float* cos, const float* sin, int64_t rope_rows,
+    const int64_t* positions, int64_t n_rows,
+    int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, float eps, int32_t dtype,
+    void* q_out, int64_t q_out_row_stride, int64_t q_out_head_stride,
+    void* k_pool, void* v_pool, int64_t pool_rows, const int64_t* write_slots,
+    void* stream) {
+  if (head_dim != kRopeD || (dtype != HX_DTYPE_BF16 && dtype != HX_DTYPE_FP16)) return HX_E_UNSUPPORTED;
+  if (n_rows < 0 || n_q_heads < 1 || n_kv_heads < 1 || rope_rows < 1 || !(eps >= 0.f)) return HX_E_INVALID_ARG;
+  if (n_rows == 0) return HX_OK;
+  if (!q || !k || !v || !q_norm_weight || !k_norm_weight || !cos || !sin || !positions || !q_out ||
+      !k_pool || !v_pool || !write_slots)
+    return HX_E_INVALID_ARG;
+  RopeArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.q_row = q_row_stride;
+  a.q_head = q_head_stride;
+  a.k_row = k_row_stride;
+  a.k_head = k_head_stride;
+  a.v_row = v_row_stride;
+  a.v_head = v_head_stride;
+  a.q_scale = q_norm_weight;
+  a.k_scale = k_norm_weight;
+  a.cos = cos;
+  a.sin = sin;
+  a.rope_rows = rope_rows;
+  a.positions = positions;
+  a.n_rows = n_rows;
+  a.hq = n_q_heads;
+  a.hkv = n_kv_heads;
+  a.eps = eps;
+  a.q_out = static_cast<uint16_t*>(q_out);
+  a.qo_row = q_out_row_stride;
+  a.qo_head = q_out_head_stride;
+  a.k_pool = static_cast<uint16_t*>(k_pool);
+  a.v_pool = static_cast<uint16_t*>(v_pool);
+  a.pool_rows = pool_rows;
+  a.slots = write_slots;
+  const int64_t items = n_rows * (n_q_heads + 2 * n_kv_heads);
+  const int64_t wgs = (items + (kRopeThreads / 64) - 1) / (kRopeThreads / 64);
+  const unsigned grid = (unsigned)(wgs < 8192 ? wgs : 8192);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == HX_DTYPE_BF16)
+    hipLaunchKernelGGL(qk_norm_rope_append_kernel<__bf16>, dim3(grid), dim3(kRopeThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(qk_norm_rope_append_kernel<_Float16>, dim3(grid), dim3(kRopeThreads), 0, s, a);
+  return hx::status_from_hip(hipGetLastError());
+}

@@ -105,6 +105,75 @@ def _check_append(k_cache, v_cache, write_slots, keys, values) -> None:
         raise ValueError("Appended K/V must have a contiguous head_dim.")
 
 
+# ----------------------------------------------------- q/k norm + RoPE + append
+def qk_norm_rope_append(
+    queries: torch.Tensor,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+    q_norm_weight: torch.Tensor,
+    k_norm_weight: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    positions: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    write_slots: torch.Tensor,
+    eps: float,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """q_norm/k_norm + apply_rope of the new rows (layers.py:146-160) fused with the KV
+    append (paged_cache.py:335-345).
+
+    ``queries`` ``[T, Hq, 128]``, ``keys``/``values`` ``[T, Hkv, 128]`` (projection
+    outputs; contiguous last dim, any row/head strides); ``q_norm_weight``/``k_norm_weight``
+    fp32 ``[128]``; ``cos``/``sin`` fp32 ``[rope_rows, 128]``; ``positions`` int64 ``[T]``
+    (flattened, e.g. ``PackedBatchCache.positions[0]``). Returns the normalised, rotated
+    queries ``[T, Hq, 128]`` (``out`` if given); rotated keys and raw values land in the
+    pools at ``write_slots``.
+    """
+    device = _require_gpu(queries, keys, values, q_norm_weight, k_norm_weight, cos, sin,
+                          positions, k_cache, v_cache, write_slots)
+    _check_append(k_cache, v_cache, write_slots, keys, values)
+    if queries.ndim != 3 or queries.shape[0] != keys.shape[0] or queries.shape[2] != keys.shape[2]:
+        raise ValueError("queries must be [tokens, q_heads, head_dim] matching the keys.")
+    if queries.dtype != keys.dtype or queries.stride(2) != 1:
+        raise ValueError("queries must share the K/V dtype and have a contiguous head_dim.")
+    head_dim = queries.shape[2]
+    for name, w in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        if w.dtype != torch.float32 or w.numel() != head_dim or not w.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 [head_dim] tensor.")
+    if (cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape
+            or cos.ndim != 2 or cos.shape[1] != head_dim or not cos.is_contiguous()
+            or not sin.is_contiguous()):
+        raise ValueError("cos/sin must be contiguous float32 [rows, head_dim] tables.")
+    positions = positions.reshape(-1)
+    if positions.dtype != torch.int64 or positions.numel() != queries.shape[0]:
+        raise ValueError("positions must be int64 with one entry per row.")
+    positions = positions.contiguous()
+    if out is None:
+        out = torch.empty(queries.shape, dtype=queries.dtype, device=device)
+    elif out.shape != queries.shape or out.dtype != queries.dtype or out.stride(2) != 1:
+        raise ValueError("out must match the queries' shape and dtype.")
+    dtype = {torch.bfloat16: _capi.HX_DTYPE_BF16, torch.float16: _capi.HX_DTYPE_FP16}.get(queries.dtype)
+    if dtype is None:
+        raise ValueError("q/k/v must be bfloat16 or float16.")
+    pool_rows = k_cache.numel() // (keys.shape[1] * head_dim)
+    code = _capi.lib().hx_qk_norm_rope_append(
+        queries.data_ptr(), queries.stride(0), queries.stride(1),
+        keys.data_ptr(), keys.stride(0), keys.stride(1),
+        values.data_ptr(), values.stride(0), values.stride(1),
+        q_norm_weight.data_ptr(), k_norm_weight.data_ptr(),
+        cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+        positions.data_ptr(), queries.shape[0],
+        queries.shape[1], keys.shape[1], head_dim, float(eps), dtype,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), pool_rows, write_slots.contiguous().data_ptr(),
+        _stream_ptr(device),
+    )
+    _capi.check(code, "hx_qk_norm_rope_append")
+    return out
+
+
 # --------------------------------------------------------------- tick metadata
 def tick_metadata(
     seq: torch.Tensor,

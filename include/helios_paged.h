@@ -250,6 +250,34 @@ size_t hx_varlen_attn_error_word_offset(void);
  * beyond sum(counts), if total_q is larger, get position -1 and slot -1). batch is at
  * most 4096.
  */
+/*
+ * Per-head RMSNorm + RoPE of the new queries and keys, fused with the KV append.
+ * Replaces, for the paged path, q_norm / k_norm and apply_rope in
+ * GroupedQueryAttention.forward (layers.py:146-160: RMSNorm over head_dim in fp32,
+ * layers.py:30-40; x * cos + cat(-x2, x1) * sin in fp32, layers.py:54-72) followed by
+ * _write (paged_cache.py:335-345). For packed row t and head h, with p = positions[t]
+ * (clamped to [0, rope_rows)) and the reference's op order (no fused multiply-adds):
+ *   n      = round((x * rsqrt(mean(x^2) + eps)) * weight)            (weight fp32 [128])
+ *   out[i] = round(n[i] * cos[p][i] - n[i+64] * sin[p][i])             i < 64
+ *   out[i] = round(n[i] * cos[p][i] + n[i-64] * sin[p][i])             i >= 64
+ * Queries go to q_out [n_rows, n_q_heads, 128] (it may alias q). Keys go to pool row
+ * write_slots[t] of k_pool, and v goes unchanged to the same row of v_pool. Rows whose
+ * slot is outside [0, pool_rows) write no K/V. cos / sin are fp32 [rope_rows, 128]
+ * tables (the model's rope_parameters buffers). head_dim must be 128; dtype is
+ * HX_DTYPE_BF16 or HX_DTYPE_FP16 for q, k, v, q_out and the pools.
+ */
+int hx_qk_norm_rope_append(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                           const void* k, int64_t k_row_stride, int64_t k_head_stride,
+                           const void* v, int64_t v_row_stride, int64_t v_head_stride,
+                           const float* q_norm_weight, const float* k_norm_weight,
+                           const float* cos, const float* sin, int64_t rope_rows,
+                           const int64_t* positions, int64_t n_rows,
+                           int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                           float eps, int32_t dtype,
+                           void* q_out, int64_t q_out_row_stride, int64_t q_out_head_stride,
+                           void* k_pool, void* v_pool, int64_t pool_rows,
+                           const int64_t* write_slots, void* stream);
+
 int hx_tick_metadata(const int32_t* seq, int32_t batch, int32_t total_q, int32_t n_logits,
                      const int32_t* block_table, int32_t block_table_stride,
                      int32_t page_size,

@@ -49,3 +49,31 @@ def packed_attention(queries: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
         )
         offset += count
     return torch.cat(outputs, dim=2)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm.forward, op for op (layers.py:36-40)."""
+    input_dtype = x.dtype
+    x = x.float()
+    normalized = x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return (normalized * weight).to(input_dtype)
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+               position_ids: torch.Tensor) -> torch.Tensor:
+    """apply_rope with position_ids, op for op (layers.py:54-72); x is [B, H, T, d] and
+    position_ids [B, T]."""
+    head_dim = x.shape[-1]
+    cos = cos[position_ids].unsqueeze(1)
+    sin = sin[position_ids].unsqueeze(1)
+    first, second = x[..., : head_dim // 2], x[..., head_dim // 2:]
+    return (x * cos + torch.cat((-second, first), dim=-1) * sin).to(x.dtype)
+
+
+def rope_parameters(head_dim: int, rows: int, base: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """rope_parameters (layers.py:43-51) for `rows` positions."""
+    inverse_frequencies = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+    positions = torch.arange(rows, dtype=torch.float32)
+    angles = positions.unsqueeze(1) * inverse_frequencies.unsqueeze(0)
+    angles = torch.cat((angles, angles), dim=1)
+    return torch.cos(angles), torch.sin(angles)
