@@ -25,6 +25,8 @@ Printed JSON (one line):
             a 4096-token chunk) and the 36-layer restore copy of 16 prefix pages.
   tick_metadata  host time of PackedBatchCache.prepare_packed with the reference's
             per-token lists and copies vs the metadata kernel, and the kernel's time.
+  norm_rope_append  q/k RMSNorm + RoPE + KV append of one layer's new rows: the
+            reference's torch op sequence vs the fused kernel (64 and 2048 rows).
   cpu_baseline  the reference's dense-KV path (gather, repeat_interleave, SDPA) in
             torch fp32 on the host cores, on one full decode layer of the same tick.
 """
@@ -319,6 +321,84 @@ def tick_metadata_leg(device, ticks: int = 20):
     return out
 
 
+def norm_rope_leg(device, reps: int = 50):
+    """q_norm/k_norm + RoPE + KV append of one layer's new rows: the reference's torch op
+    sequence (layers.py:146-160, then _write's two index_copy_) vs the fused kernel, for
+    the 64-row decode tick and the 2048-row mixed tick."""
+    import torch
+
+    from helios_amd import ops
+    from oracle import dense_torch
+
+    d, hq, hkv = 128, 32, 8
+    cos, sin = dense_torch.rope_parameters(d, 40960, 1_000_000.0)
+    cos, sin = cos.to(device), sin.to(device)
+    g = torch.Generator(device=device).manual_seed(3)
+    out = {}
+    for rows in (64, 2048):
+        proj = torch.randn((1, rows, (hq + 2 * hkv) * d), generator=g, device=device).to(torch.bfloat16)
+        q = proj[..., : hq * d].view(1, rows, hq, d)
+        k = proj[..., hq * d:(hq + hkv) * d].view(1, rows, hkv, d)
+        v = proj[..., (hq + hkv) * d:].view(1, rows, hkv, d)
+        wq = torch.ones(d, device=device)
+        wk = torch.ones(d, device=device)
+        positions = torch.randint(0, 8192, (1, rows), generator=g, device=device)
+        k_pool = torch.zeros((2048, 256, hkv, d), device=device, dtype=torch.bfloat16)
+        v_pool = torch.zeros_like(k_pool)
+        slots = torch.randperm(2048 * 256, generator=g, device=device)[:rows]
+
+        def reference():
+            qq = dense_torch.apply_rope(dense_torch.rms_norm(q.transpose(1, 2), wq, 1e-6), cos, sin, positions)
+            kk = dense_torch.apply_rope(dense_torch.rms_norm(k.transpose(1, 2), wk, 1e-6), cos, sin, positions)
+            pk = kk.transpose(1, 2).reshape(-1, hkv, d)
+            pv = v.reshape(-1, hkv, d)
+            k_pool.view(-1, hkv, d).index_copy_(0, slots, pk)
+            v_pool.view(-1, hkv, d).index_copy_(0, slots, pv)
+            return qq
+
+        def fused():
+            return ops.qk_norm_rope_append(q[0], k[0], v[0], wq, wk, cos, sin, positions, k_pool,
+                                           v_pool, slots, 1e-6)
+
+        res = {}
+        for name, fn in (("reference_ops", reference), ("fused_kernel", fused)):
+            # Device time: 10 calls captured in a HIP graph and replayed, so host launch
+            # overhead does not leave the GPU idle between them.
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    fn()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(10):
+                    fn()
+            graph.replay()
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            for a, b in ev:
+                a.record()
+                graph.replay()
+                b.record()
+            torch.cuda.synchronize()
+            res[f"{name}_gpu_us"] = round(statistics.median(a.elapsed_time(b) for a, b in ev) * 1e3 / 10, 2)
+            # Host time of one eager call (what the scheduler thread spends launching).
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fn()
+            t1 = time.perf_counter()
+            torch.cuda.synchronize()
+            res[f"{name}_host_us"] = round((t1 - t0) / reps * 1e6, 1)
+            del graph
+        nbytes = rows * (hq + 2 * hkv) * d * 2 * 2 + rows * 2 * d * 4 * 2
+        res["fused_gbs"] = round(nbytes / (res["fused_kernel_gpu_us"] * 1e-6) / 1e9, 1)
+        out[f"rows_{rows}"] = res
+        del k_pool, v_pool, proj
+        torch.cuda.empty_cache()
+    return out
+
+
 def pmc_pass(device):
     """Counter-collection run: a page copy of known size, then decode-tick steps, then
     mixed-tick and long-context steps (their chunk launches carry the MFMA counters)."""
@@ -450,6 +530,7 @@ def main():
         result["packed_tick"] = packed_tick(device)
         result["long_context"] = long_context(device)
         result["tick_metadata"] = tick_metadata_leg(device)
+        result["norm_rope_append"] = norm_rope_leg(device)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)

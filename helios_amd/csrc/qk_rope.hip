@@ -8,8 +8,8 @@
 // keys are normalised, rotated and stored straight into their pool rows, and values are
 // copied into theirs; the rotated keys never make a round trip through HBM.
 //
-// One wave per (row, head); lane l owns dims l and l + 64, which are exactly the pair
-// that RoPE mixes. The arithmetic follows the reference's op order with no fused
+// One workgroup per packed row, one wave per head at a time; lane l owns dims l and
+// l + 64, which are exactly the pair that RoPE mixes. The arithmetic follows the reference's op order with no fused
 // multiply-adds: n = bf16((x * rsqrt(mean(x^2) + eps)) * w), then
 // out = bf16(n * cos + (-n') * sin).
 
@@ -53,23 +53,29 @@ __device__ __forceinline__ uint16_t from_f(float f) {
 
 template <typename T>
 __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_append_kernel(RopeArgs a) {
+  // One workgroup per packed row: the row's position, slot, RoPE factors and norm
+  // weights are read once and reused by every head; wave w takes heads w, w + 4, ...
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = blockIdx.x;
   const int heads = a.hq + 2 * a.hkv;
-  const int64_t items = a.n_rows * heads;
-  const int64_t step = (int64_t)gridDim.x * (kRopeThreads / 64);
-  for (int64_t it = (int64_t)blockIdx.x * (kRopeThreads / 64) + wave; it < items; it += step) {
-    const int64_t row = it / heads;
-    const int h = (int)(it - row * heads);
-    const int64_t slot = a.slots[row];
-    const bool slot_ok = slot >= 0 && slot < a.pool_rows;
+  const int64_t slot = a.slots[row];
+  const bool slot_ok = slot >= 0 && slot < a.pool_rows;
+  int64_t pos = a.positions[row];
+  pos = pos < 0 ? 0 : (pos >= a.rope_rows ? a.rope_rows - 1 : pos);
+  const float c0 = a.cos[pos * kRopeD + lane], c1 = a.cos[pos * kRopeD + lane + 64];
+  const float s0 = a.sin[pos * kRopeD + lane], s1 = a.sin[pos * kRopeD + lane + 64];
+  const float wq0 = a.q_scale[lane], wq1 = a.q_scale[lane + 64];
+  const float wk0 = a.k_scale[lane], wk1 = a.k_scale[lane + 64];
+  for (int h = wave; h < heads; h += kRopeThreads / 64) {
     if (h >= a.hq + a.hkv) {  // value head: plain copy into the pool
       if (!slot_ok) continue;
       const int hv = h - a.hq - a.hkv;
       const uint16_t* src = a.v + row * a.v_row + hv * a.v_head;
       uint16_t* dst = a.v_pool + (slot * a.hkv + hv) * kRopeD;
-      dst[lane] = src[lane];
-      dst[lane + 64] = src[lane + 64];
+      const uint16_t e0 = src[lane], e1 = src[lane + 64];
+      dst[lane] = e0;
+      dst[lane + 64] = e1;
       continue;
     }
     const bool is_q = h < a.hq;
@@ -80,15 +86,10 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_append_kernel(RopeA
     float ss = __fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1));
     for (int m = 32; m >= 1; m >>= 1) ss = __fadd_rn(ss, __shfl_xor(ss, m));
     const float r = rsqrtf(__fadd_rn(__fdiv_rn(ss, (float)kRopeD), a.eps));
-    const float* w = is_q ? a.q_scale : a.k_scale;
-    const float n0 = to_f<T>(from_f<T>(__fmul_rn(__fmul_rn(x0, r), w[lane])));
-    const float n1 = to_f<T>(from_f<T>(__fmul_rn(__fmul_rn(x1, r), w[lane + 64])));
-    int64_t pos = a.positions[row];
-    pos = pos < 0 ? 0 : (pos >= a.rope_rows ? a.rope_rows - 1 : pos);
-    const float* c = a.cos + pos * kRopeD;
-    const float* s = a.sin + pos * kRopeD;
-    const float o0 = __fadd_rn(__fmul_rn(n0, c[lane]), __fmul_rn(-n1, s[lane]));
-    const float o1 = __fadd_rn(__fmul_rn(n1, c[lane + 64]), __fmul_rn(n0, s[lane + 64]));
+    const float n0 = to_f<T>(from_f<T>(__fmul_rn(__fmul_rn(x0, r), is_q ? wq0 : wk0)));
+    const float n1 = to_f<T>(from_f<T>(__fmul_rn(__fmul_rn(x1, r), is_q ? wq1 : wk1)));
+    const float o0 = __fadd_rn(__fmul_rn(n0, c0), __fmul_rn(-n1, s0));
+    const float o1 = __fadd_rn(__fmul_rn(n1, c1), __fmul_rn(n0, s1));
     uint16_t* dst = is_q ? a.q_out + row * a.qo_row + hh * a.qo_head
                          : a.k_pool + (slot * a.hkv + hh) * kRopeD;
     dst[lane] = from_f<T>(o0);
@@ -142,9 +143,8 @@ extern "C" int hx_qk_norm_rope_append(
   a.v_pool = static_cast<uint16_t*>(v_pool);
   a.pool_rows = pool_rows;
   a.slots = write_slots;
-  const int64_t items = n_rows * (n_q_heads + 2 * n_kv_heads);
-  const int64_t wgs = (items + (kRopeThreads / 64) - 1) / (kRopeThreads / 64);
-  const unsigned grid = (unsigned)(wgs < 8192 ? wgs : 8192);
+  if (n_rows > 0x7fffffff) return HX_E_INVALID_ARG;
+  const unsigned grid = (unsigned)n_rows;  // one workgroup per packed row
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (dtype == HX_DTYPE_BF16)
     hipLaunchKernelGGL(qk_norm_rope_append_kernel<__bf16>, dim3(grid), dim3(kRopeThreads), 0, s, a);
