@@ -27,6 +27,9 @@ Printed JSON (one line):
             per-token lists and copies vs the metadata kernel, and the kernel's time.
   norm_rope_append  q/k RMSNorm + RoPE + KV append of one layer's new rows: the
             reference's torch op sequence vs the fused kernel (64 and 2048 rows).
+  full_tick  a full random-init Qwen3-4B continuous-batching tick (128 decoders + a
+            1024-token chunk, shared prefix pages): tokens/s and the attention step's
+            share, for this build's path and for the reference's op sequence.
   cpu_baseline  the reference's dense-KV path (gather, repeat_interleave, SDPA) in
             torch fp32 on the host cores, on one full decode layer of the same tick.
 """
@@ -56,6 +59,8 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-packed-tick", action="store_true")
+    p.add_argument("--full-tick", action=argparse.BooleanOptionalAction, default=True,
+                   help="full random-init Qwen3-4B tick (128 decoders + a 1024-token chunk)")
     p.add_argument("--pmc-pass", action="store_true",
                    help="short run for rocprofv3 counter collection: a calibration page "
                         "copy of known size, then a few decode steps")
@@ -399,6 +404,88 @@ def norm_rope_leg(device, reps: int = 50):
     return out
 
 
+def full_tick_leg(device, ticks: int = 4, seed: int = 5):
+    """Full random-init Qwen3-4B forward of one continuous-batching tick: 128 decoders
+    (contexts uniform in 1024-8192, each sharing up to 16 pages of a 4096-token system
+    prefix) plus one 1024-token prefill chunk that also starts from the shared prefix;
+    1152 packed tokens, one logit row per sequence. Every tick is rolled back with
+    truncate() so each timed tick is the same. Reports tokens/s of the whole tick and
+    the attention step's share (q/k norm + RoPE + KV append + paged attention), for
+    this build's path (metadata kernel, fused norm/RoPE/append) and for the reference's
+    sequence on the same kernels (host metadata lists, torch norm/RoPE, attend)."""
+    import numpy as np
+    import torch
+
+    from helios_amd.config import Qwen3Config
+    from helios_amd.decoder import PagedQwen3Decoder
+    from helios_amd.paged_cache import KVPagePool, PackedBatchCache, PagedKVCache
+
+    config = Qwen3Config()
+    rng = np.random.default_rng(seed)
+    ctx = [int(x) for x in rng.integers(1024, 8193, 128)]
+    prefix_pages = 16
+    own_pages = sum(-(-c // 256) - min(prefix_pages, (c - 1) // 256) + 1 for c in ctx) + 8
+    num_pages = prefix_pages + own_pages + 8
+    model = PagedQwen3Decoder(config, device, seed=seed)
+    pool = KVPagePool(config, num_pages, device=device)
+    g = torch.Generator(device=device).manual_seed(seed)
+    for t in pool.keys + pool.values:
+        t.normal_(generator=g)
+    prefix = PagedKVCache(pool, config.context_length)
+    prefix.pages.extend(pool.acquire(prefix_pages))
+    prefix.length = prefix_pages * 256
+    caches, lengths = [], []
+    for c in ctx + [None]:
+        cache = PagedKVCache(pool, config.context_length)
+        cached = c - 1 if c is not None else prefix.length
+        shared = min(prefix_pages, cached // 256)
+        cache.pages.extend(prefix.pages[:shared])
+        cache.pages.extend(pool.acquire(-(-cached // 256) - shared))
+        cache.length = cached
+        caches.append(cache)
+        lengths.append(cached)
+    counts = [1] * len(ctx) + [1024]
+    tokens = sum(counts)
+    input_ids = torch.randint(0, config.vocab_size, (1, tokens), generator=g, device=device)
+
+    def tick(batch, fused, events=None):
+        batch.prepare_packed(counts)
+        logits = model.forward_packed(input_ids, batch, fused_rope=fused, attention_events=events)
+        for cache, n in zip(caches, lengths):
+            cache.truncate(n)
+        return logits
+
+    res = {"workload": "Qwen3-4B random-init bf16, 36 layers: 128 decoders ctx U[1024,8192] "
+                       "sharing <=16 pages of a 4096-token prefix + one 1024-token chunk after "
+                       "that prefix; 1152 packed tokens", "tokens": tokens}
+    for name, device_meta, fused in (("this_build", True, True), ("reference_sequence", False, False)):
+        batch = PackedBatchCache(caches, device_metadata=device_meta)
+        for _ in range(2):
+            tick(batch, fused)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(ticks):
+            logits = tick(batch, fused)
+        torch.cuda.synchronize()
+        sec = (time.perf_counter() - t0) / ticks
+        events = []
+        tick(batch, fused, events)
+        torch.cuda.synchronize()
+        attn_ms = sum(a.elapsed_time(b) for a, b in events)
+        res[name] = {
+            "ms_per_tick": round(sec * 1e3, 3),
+            "tokens_per_s": round(tokens / sec, 1),
+            "decode_tokens_per_s": round(len(ctx) / sec, 1),
+            "attention_ms_per_tick": round(attn_ms, 3),
+            "attention_share": round(attn_ms / (sec * 1e3), 4),
+        }
+        assert torch.isfinite(logits.float()).all()
+        del batch
+    del model, pool, caches, prefix
+    torch.cuda.empty_cache()
+    return res
+
+
 def pmc_pass(device):
     """Counter-collection run: a page copy of known size, then decode-tick steps, then
     mixed-tick and long-context steps (their chunk launches carry the MFMA counters)."""
@@ -531,6 +618,8 @@ def main():
         result["long_context"] = long_context(device)
         result["tick_metadata"] = tick_metadata_leg(device)
         result["norm_rope_append"] = norm_rope_leg(device)
+    if args.full_tick:
+        result["full_tick"] = full_tick_leg(device)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)
