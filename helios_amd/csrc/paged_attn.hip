@@ -19,12 +19,14 @@
 //                   write partials: fp32 (m, l) and o / l rounded to bf16 (the partial
 //                   stores cost more than their 1.6% of the bytes suggests, so they are
 //                   halved; the extra error is one more bf16 rounding of the output).
-//   combine_kernel  merges the partials of each long decode sequence in split order, so
-//                   results do not depend on scheduling.
 //   chunk_kernel    prefill chunks: 8 waves per workgroup (2 per SIMD), each wave owning
 //                   32 query rows of one head; 64-key K / V^T tiles go through LDS with a
 //                   register prefetch of the next tile; S^T = K Q^T and O^T = V^T P^T both
-//                   run on 16x16x32 MFMA with online softmax in between.
+//                   run on 16x16x32 MFMA with online softmax in between. When the chunk
+//                   rows alone would not fill the GPU, row blocks are split over their key
+//                   tiles and write partials like decode splits.
+//   combine_kernel  merges the partials of each long decode row and each split chunk row
+//                   in split order, so results do not depend on scheduling. Runs last.
 
 #include "hx_common.h"
 
@@ -37,6 +39,14 @@ constexpr int kSplit = 256;      // keys per decode workgroup
 constexpr int kThreads = 256;    // 4 wavefronts
 constexpr int kTile = 64;        // keys per chunk-kernel tile
 constexpr int kPlanThreads = 1024;
+// Chunk split-K: when the chunk work items would launch fewer than kChunkFillWGs
+// workgroups, each row block's key tiles are cut into splits of at least
+// kMinSplitTiles tiles so that about kChunkFillWGs workgroups run; split partials are
+// merged by the combine kernel like decode splits.
+constexpr int kChunkFillWGs = 512;
+constexpr int kMinSplitTiles = 8;
+constexpr int kMaxChunkSplits = 64;
+constexpr int kCombRows = 8;  // output rows per combine record of a split chunk block
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -67,25 +77,70 @@ inline Geometry geometry(int hq, int hkv) {
 }
 
 struct Layout {
-  size_t seq_info, dec_items, comb_seqs, pf_items, part_ml, part_o, total;
-  int64_t max_dec, max_pf;
+  size_t seq_info, dec_items, comb_seqs, pf_items, pf_base, part_ml, part_o, total;
+  int64_t max_dec, max_pf, max_comb, cslot_cap;
 };
 
+// Partial slots: decode splits use [0, max_dec), chunk split rows [max_dec, + cslot_cap).
+// Splitting happens only while the unsplit items launch < kChunkFillWGs workgroups, and
+// the split size keeps the split items near that many, so sum over row blocks of the
+// split count is below 2 * kChunkFillWGs / (hkv * head_quads): that bounds the chunk
+// partial rows, and each split adds at most one item per block and head quad.
 inline Layout make_layout(int batch, int max_q, int max_k, int hq, int hkv) {
   const Geometry geo = geometry(hq, hkv);
   Layout l;
   const int64_t splits = max_k > 0 ? ceil_div(max_k, kSplit) : 1;
   l.max_dec = (int64_t)batch * splits;
-  l.max_pf = max_q >= 2 ? (int64_t)batch * ceil_div(max_q, geo.rows_per_item) * geo.head_quads : 0;
+  l.max_pf = 0;
+  l.cslot_cap = 0;
+  if (max_q >= 2) {
+    l.max_pf = (int64_t)batch * ceil_div(max_q, geo.rows_per_item) * geo.head_quads + 2 * kChunkFillWGs;
+    l.cslot_cap = ceil_div(2 * kChunkFillWGs, (int64_t)hkv * geo.head_quads) * geo.rows_per_item;
+  }
+  l.max_comb = (int64_t)batch + l.cslot_cap;
   size_t off = align256(H_WORDS * sizeof(int32_t));
   l.seq_info = off;  off = align256(off + (size_t)batch * sizeof(int4));
   l.dec_items = off; off = align256(off + (size_t)l.max_dec * sizeof(int4));
-  l.comb_seqs = off; off = align256(off + (size_t)batch * sizeof(int4));
+  l.comb_seqs = off; off = align256(off + (size_t)l.max_comb * sizeof(int4));
   l.pf_items = off;  off = align256(off + (size_t)l.max_pf * sizeof(int4));
-  l.part_ml = off;   off = align256(off + (size_t)l.max_dec * hq * sizeof(float2));
-  l.part_o = off;    off = align256(off + (size_t)l.max_dec * hq * kD * sizeof(uint16_t));
+  l.pf_base = off;   off = align256(off + (size_t)l.max_pf * sizeof(int32_t));
+  const int64_t slots = l.max_dec + l.cslot_cap;
+  l.part_ml = off;   off = align256(off + (size_t)slots * hq * sizeof(float2));
+  l.part_o = off;    off = align256(off + (size_t)slots * hq * kD * sizeof(uint16_t));
   l.total = off;
   return l;
+}
+
+// Key tiles [*tb, *te) of the chunk row block starting at row0 (rows_per_item rows) of a
+// sequence with n query rows and L keys, under the (left, right) window.
+__host__ __device__ inline void chunk_tiles(int n, int L, int row0, int rows_per_item, int win_left,
+                                            int win_right, int* tb, int* te) {
+  const int off = L - n;
+  const int row_end = n < row0 + rows_per_item ? n : row0 + rows_per_item;
+  int klo = 0;
+  if (win_left >= 0) {
+    klo = off + row0 - win_left;
+    if (klo < 0) klo = 0;
+  }
+  int khi = L - 1;
+  if (win_right >= 0 && off + row_end - 1 + win_right < khi) khi = off + row_end - 1 + win_right;
+  *tb = klo / kTile;
+  *te = khi >= klo ? khi / kTile + 1 : *tb;
+}
+
+// Tiles per chunk split for a tick whose chunk items total `items` (row blocks x head
+// quads) and `tiles` key tiles: 0 when the items already launch kChunkFillWGs
+// workgroups (no split).
+__host__ __device__ inline int chunk_split_tiles(int64_t tiles, int64_t items, int hkv) {
+  if (items == 0 || items * hkv >= kChunkFillWGs) return 0;
+  int64_t t = (tiles * hkv + kChunkFillWGs - 1) / kChunkFillWGs;
+  return (int)(t > kMinSplitTiles ? t : kMinSplitTiles);
+}
+
+__host__ __device__ inline int chunk_split_count(int tiles, int split_tiles) {
+  if (split_tiles <= 0 || tiles <= split_tiles) return 1;
+  const int s = (tiles + split_tiles - 1) / split_tiles;
+  return s < kMaxChunkSplits ? s : kMaxChunkSplits;
 }
 
 // Decode key window of a one-token row at position L-1: keys [lo, L).
@@ -118,8 +173,9 @@ struct PlanArgs {
   int4* dec_items;
   int4* comb_seqs;
   int4* pf_items;
+  int32_t* pf_base;
   int64_t total_k_rows;
-  int64_t max_dec, max_pf;
+  int64_t max_dec, max_pf, max_comb, cslot_cap;
   int32_t batch, total_q, max_q, max_k;
   int32_t page_size, bt_stride;
   int32_t rows_per_item, head_quads;
@@ -148,101 +204,171 @@ __device__ int block_exclusive_scan(int v, int* wave_tot, int* total) {
   return pre + x - v;
 }
 
+// Per-sequence metadata with the bounds checks of every run kernel: rows [q0, q0 + n),
+// L keys, packed-key base kvb; error bits for anything clamped.
+struct SeqMeta {
+  int q0, n, L, kvb;
+};
+__device__ SeqMeta plan_seq(const PlanArgs& a, int b, int& err) {
+  SeqMeta m{0, 0, 0, 0};
+  m.q0 = a.cu_q[b];
+  const int q1 = a.cu_q[b + 1];
+  if (m.q0 < 0 || q1 < m.q0 || q1 > a.total_q) {
+    err |= HX_WERR_BAD_CU_SEQ;
+    m.q0 = 0;
+    m.n = 0;
+  } else {
+    m.n = q1 - m.q0;
+  }
+  if (m.n > a.max_q) {
+    err |= HX_WERR_CLAMPED_LEN;
+    m.n = a.max_q;
+  }
+  m.L = a.used_k ? a.used_k[b] : a.cu_k[b + 1] - a.cu_k[b];
+  if (m.L < 0) {
+    err |= HX_WERR_CLAMPED_LEN;
+    m.L = 0;
+  }
+  if (m.L > a.max_k) {
+    err |= HX_WERR_CLAMPED_LEN;
+    m.L = a.max_k;
+  }
+  if (a.page_size > 0) {
+    const int64_t cap = (int64_t)a.bt_stride * a.page_size;
+    if (m.L > cap) {
+      err |= HX_WERR_CLAMPED_LEN;
+      m.L = (int)cap;
+    }
+  } else {
+    m.kvb = a.cu_k[b];
+    if (m.kvb < 0 || m.kvb > a.total_k_rows) {
+      err |= HX_WERR_CLAMPED_LEN;
+      m.kvb = 0;
+      m.L = 0;
+    } else if ((int64_t)m.kvb + m.L > a.total_k_rows) {
+      err |= HX_WERR_CLAMPED_LEN;
+      m.L = (int)(a.total_k_rows - m.kvb);
+    }
+  }
+  return m;
+}
+
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
   __shared__ int wave_tot[kPlanThreads / 64];
   __shared__ int err_bits;
   if (threadIdx.x == 0) err_bits = 0;
   __syncthreads();
-  int base_dec = 0, base_pf = 0, base_comb = 0;
   int err = 0;
+
+  // Pass 1: chunk work before splitting (items and key tiles, head quads counted).
+  int64_t pf_items0 = 0, pf_tiles = 0;
+  for (int b0 = 0; b0 < a.batch; b0 += kPlanThreads) {
+    const int b = b0 + (int)threadIdx.x;
+    int items = 0, tiles = 0;
+    if (b < a.batch) {
+      int e = 0;
+      const SeqMeta m = plan_seq(a, b, e);
+      if (m.n >= 2) {
+        for (int row0 = 0; row0 < m.n; row0 += a.rows_per_item) {
+          int tb, te;
+          chunk_tiles(m.n, m.L, row0, a.rows_per_item, a.win_left, a.win_right, &tb, &te);
+          tiles += (te - tb) * a.head_quads;
+          items += a.head_quads;
+        }
+      }
+    }
+    int tot_i, tot_t;
+    block_exclusive_scan(items, wave_tot, &tot_i);
+    block_exclusive_scan(tiles, wave_tot, &tot_t);
+    pf_items0 += tot_i;
+    pf_tiles += tot_t;
+  }
+  const int split_tiles = chunk_split_tiles(pf_tiles, pf_items0, a.hkv);
+
+  // Pass 2: work lists.
+  int base_dec = 0, base_pf = 0, base_comb = 0, base_slot = 0;
   for (int b0 = 0; b0 < a.batch; b0 += kPlanThreads) {
     const int b = b0 + (int)threadIdx.x;
     const bool active = b < a.batch;
-    int q0 = 0, n = 0, L = 0, kvb = 0;
-    if (active) {
-      q0 = a.cu_q[b];
-      const int q1 = a.cu_q[b + 1];
-      if (q0 < 0 || q1 < q0 || q1 > a.total_q) {
-        err |= HX_WERR_BAD_CU_SEQ;
-        q0 = 0;
-        n = 0;
-      } else {
-        n = q1 - q0;
-      }
-      if (n > a.max_q) {
-        err |= HX_WERR_CLAMPED_LEN;
-        n = a.max_q;
-      }
-      if (a.used_k) {
-        L = a.used_k[b];
-      } else {
-        L = a.cu_k[b + 1] - a.cu_k[b];
-      }
-      if (L < 0) {
-        err |= HX_WERR_CLAMPED_LEN;
-        L = 0;
-      }
-      if (L > a.max_k) {
-        err |= HX_WERR_CLAMPED_LEN;
-        L = a.max_k;
-      }
-      if (a.page_size > 0) {
-        const int64_t cap = (int64_t)a.bt_stride * a.page_size;
-        if (L > cap) {
-          err |= HX_WERR_CLAMPED_LEN;
-          L = (int)cap;
-        }
-      } else {
-        kvb = a.cu_k[b];
-        if (kvb < 0 || kvb > a.total_k_rows) {
-          err |= HX_WERR_CLAMPED_LEN;
-          kvb = 0;
-          L = 0;
-        } else if ((int64_t)kvb + L > a.total_k_rows) {
-          err |= HX_WERR_CLAMPED_LEN;
-          L = (int)(a.total_k_rows - kvb);
-        }
-      }
-    }
-    int nd = 0, np = 0, nc = 0, s_first = 0, splits = 0, nblk = 0;
-    if (active && n == 1) {
-      decode_splits(L, a.win_left, &s_first, &splits);
+    SeqMeta m{0, 0, 0, 0};
+    if (active) m = plan_seq(a, b, err);
+    int nd = 0, np = 0, nc = 0, ns = 0, s_first = 0, splits = 0, nblk = 0;
+    if (active && m.n == 1) {
+      decode_splits(m.L, a.win_left, &s_first, &splits);
       nd = splits;
       nc = splits > 1 ? 1 : 0;
-    } else if (active && n >= 2) {
-      nblk = (n + a.rows_per_item - 1) / a.rows_per_item;
-      np = nblk * a.head_quads;
+    } else if (active && m.n >= 2) {
+      nblk = (m.n + a.rows_per_item - 1) / a.rows_per_item;
+      for (int blk = 0; blk < nblk; ++blk) {
+        const int row0 = blk * a.rows_per_item;
+        int tb, te;
+        chunk_tiles(m.n, m.L, row0, a.rows_per_item, a.win_left, a.win_right, &tb, &te);
+        const int S = chunk_split_count(te - tb, split_tiles);
+        const int rows = min(a.rows_per_item, m.n - row0);
+        np += S * a.head_quads;
+        if (S > 1) {
+          ns += rows * S;
+          nc += (rows + kCombRows - 1) / kCombRows;
+        }
+      }
     }
-    int tot_d, tot_p, tot_c;
+    int tot_d, tot_p, tot_c, tot_s;
     const int off_d = base_dec + block_exclusive_scan(nd, wave_tot, &tot_d);
     const int off_p = base_pf + block_exclusive_scan(np, wave_tot, &tot_p);
     const int off_c = base_comb + block_exclusive_scan(nc, wave_tot, &tot_c);
+    const int off_s = base_slot + block_exclusive_scan(ns, wave_tot, &tot_s);
     if (active) {
-      a.seq_info[b] = make_int4(q0, n, L, kvb);
+      a.seq_info[b] = make_int4(m.q0, m.n, m.L, m.kvb);
       for (int k = 0; k < nd; ++k) {
-        if (off_d + k < a.max_dec) a.dec_items[off_d + k] = make_int4(b, s_first + k, q0, L);
+        if (off_d + k < a.max_dec) a.dec_items[off_d + k] = make_int4(b, s_first + k, m.q0, m.L);
       }
-      if (nc) a.comb_seqs[off_c] = make_int4(b, off_d, splits, q0);
-      // Later row blocks see more keys under a causal mask: list them first.
-      int k = 0;
-      for (int blk = nblk - 1; blk >= 0; --blk) {
-        for (int hq = 0; hq < a.head_quads; ++hq, ++k) {
-          if (off_p + k < a.max_pf) a.pf_items[off_p + k] = make_int4(b, blk * a.rows_per_item, hq, 0);
+      if (nc && m.n == 1 && off_c < a.max_comb) a.comb_seqs[off_c] = make_int4(b, off_d, splits, m.q0);
+      if (m.n >= 2) {
+        // Later row blocks see more keys under a causal mask: list them first. A split
+        // block's rows own S consecutive partial slots each, merged by one combine
+        // record per row.
+        int k = 0, slot = off_s, comb = off_c;
+        for (int blk = nblk - 1; blk >= 0; --blk) {
+          const int row0 = blk * a.rows_per_item;
+          int tb, te;
+          chunk_tiles(m.n, m.L, row0, a.rows_per_item, a.win_left, a.win_right, &tb, &te);
+          const int S = chunk_split_count(te - tb, split_tiles);
+          const int rows = min(a.rows_per_item, m.n - row0);
+          const bool fits = S == 1 || slot + rows * S <= a.cslot_cap;
+          if (!fits) err |= HX_WERR_GRID;
+          for (int hq = 0; hq < a.head_quads; ++hq) {
+            for (int sp = 0; sp < S; ++sp, ++k) {
+              if (off_p + k < a.max_pf) {
+                a.pf_items[off_p + k] = make_int4(b, row0, hq, fits ? (sp | ((S - 1) << 16)) : 0);
+                a.pf_base[off_p + k] = slot;
+              }
+            }
+          }
+          if (S > 1) {
+            for (int r = 0; r < rows; r += kCombRows, ++comb) {
+              const int nr = min(kCombRows, rows - r);
+              if (fits && comb < a.max_comb)
+                a.comb_seqs[comb] = make_int4(b, (int)a.max_dec + slot + r * S, S | ((nr - 1) << 24),
+                                              m.q0 + row0 + r);
+            }
+            slot += rows * S;
+          }
         }
       }
     }
     base_dec += tot_d;
     base_pf += tot_p;
     base_comb += tot_c;
+    base_slot += tot_s;
   }
   if (err) atomicOr(&err_bits, err);
   __syncthreads();
   if (threadIdx.x == 0) {
     int e = err_bits;
-    if (base_dec > a.max_dec || base_pf > a.max_pf) e |= HX_WERR_GRID;
+    if (base_dec > a.max_dec || base_pf > a.max_pf || base_comb > a.max_comb) e |= HX_WERR_GRID;
     a.hdr[H_NDEC] = base_dec < a.max_dec ? base_dec : (int)a.max_dec;
     a.hdr[H_NPF] = base_pf < a.max_pf ? base_pf : (int)a.max_pf;
-    a.hdr[H_NCOMB] = base_comb;
+    a.hdr[H_NCOMB] = base_comb < a.max_comb ? base_comb : (int)a.max_comb;
     a.hdr[H_ERR] = e;
     a.hdr[H_BATCH] = a.batch;
     a.hdr[H_MAXQ] = a.max_q;
@@ -266,8 +392,11 @@ struct RunArgs {
   const int4* dec_items;
   const int4* comb_seqs;
   const int4* pf_items;
-  float2* part_ml;   // per (split, head): running max m (log2 units) and sum l
-  uint16_t* part_o;  // per (split, head, dim): o / l as bf16
+  const int32_t* pf_base;  // per chunk item: first partial row of its block (split blocks)
+  float2* part_ml;   // per (slot, head): running max m (log2 units) and sum l
+  uint16_t* part_o;  // per (slot, head, dim): o / l as bf16
+  int64_t dec_cap;   // decode slots [0, dec_cap); chunk split rows follow
+  int64_t slot_cap;  // all partial slots
   int64_t q_row, q_head;     // element strides
   int64_t kv_row, kv_head;
   int64_t o_row, o_head;
@@ -597,62 +726,85 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
 }
 
 // ------------------------------------------------------------------ split combine
-// One thread per (head, dim) output: the partial rows of a sequence are merged with an
-// online max in chunks of 16 splits, each chunk's 16 (m, l) pairs and 16 partial values
-// loaded together, so a sequence of up to 16 splits costs one memory round trip.
+// A combine record {b, first slot, splits | (rows - 1) << 24, first output row} covers
+// `rows` consecutive output rows (1 for a decode row, up to kCombRows rows of a split
+// chunk block) whose partials sit at slots first + r * splits + s. One thread per (row,
+// head, 8-dim chunk): 16-byte partial loads, merged with an online max in groups of
+// kCombChunk splits whose (m, l) pairs and partial rows are loaded together.
+constexpr int kCombChunk = 8;
+
 template <typename T, int G>
 __global__ __launch_bounds__(kThreads) void combine_kernel(RunArgs a) {
-  typedef hx::Elem<T> E;
-  constexpr int kChunk = 16;
+  constexpr int kPerRow = G * (kD / 8);  // threads per output row
   const int cs = (int)blockIdx.x / a.hkv;
   const int g = (int)blockIdx.x - cs * a.hkv;
   const Header hd = read_header(a);
-  const int4 c = a.comb_seqs[cs];  // {b, first item, splits, q0}; cs < grid_comb <= batch
+  const int4 c = a.comb_seqs[cs];  // cs < grid_comb <= max_comb
   if (!hd.ok) return;
   const int n_comb = hd.counts.z;
   if (blockIdx.x == 0 && threadIdx.x == 0 && n_comb > a.grid_comb) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
   if (cs >= n_comb) return;
-  const int first = c.y, splits = c.z, q0 = c.w;
-  if ((unsigned)c.x >= (unsigned)a.batch || first < 0 || splits < 1) return;
-  if ((int64_t)first + splits > (int64_t)hd.counts.x) return;
-  for (int oi = threadIdx.x; oi < G * kD; oi += kThreads) {
-    const int h = oi >> 7, d = oi & (kD - 1);
+  const int first = c.y, splits = c.z & 0xffffff, rows = (c.z >> 24) + 1, q0 = c.w;
+  if ((unsigned)c.x >= (unsigned)a.batch || first < 0 || splits < 1 || rows > kCombRows) return;
+  if ((int64_t)first + (int64_t)rows * splits > a.slot_cap) return;
+  if (q0 < 0 || q0 + rows > a.total_q) return;
+  for (int t = threadIdx.x; t < rows * kPerRow; t += kThreads) {
+    const int r = t / kPerRow;
+    const int h = (t - r * kPerRow) >> 4, ch = t & 15;
     const int qh = g * G + h;
-    const float2* ml = a.part_ml + (int64_t)first * a.hq + qh;
-    const uint16_t* po = a.part_o + ((int64_t)first * a.hq + qh) * kD + d;
+    const int64_t base = (int64_t)first + (int64_t)r * splits;
+    const float2* ml = a.part_ml + base * a.hq + qh;
+    const uint16_t* po = a.part_o + (base * a.hq + qh) * kD + 8 * ch;
     const int64_t step_o = (int64_t)a.hq * kD;
-    float m_run = -INFINITY, l_run = 0.f, acc = 0.f;
-    for (int s0 = 0; s0 < splits; s0 += kChunk) {
-      float2 mlv[kChunk];
-      float ov[kChunk];
+    float m_run = -INFINITY, l_run = 0.f;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < splits; s0 += kCombChunk) {
+      float2 mlv[kCombChunk];
+      uint4 ov[kCombChunk];
 #pragma unroll
-      for (int j = 0; j < kChunk; ++j) {
+      for (int j = 0; j < kCombChunk; ++j) {
         const int sj = s0 + j < splits ? s0 + j : splits - 1;  // clamp: duplicates get weight 0
         mlv[j] = ml[(int64_t)sj * a.hq];
-        ov[j] = __uint_as_float((uint32_t)po[(int64_t)sj * step_o] << 16);
+        ov[j] = *reinterpret_cast<const uint4*>(po + (int64_t)sj * step_o);
       }
       float cm = m_run;
 #pragma unroll
-      for (int j = 0; j < kChunk; ++j)
+      for (int j = 0; j < kCombChunk; ++j)
         if (s0 + j < splits) cm = fmaxf(cm, mlv[j].x);
       if (cm != -INFINITY) {
         const float rescale = m_run == -INFINITY ? 0.f : hx::fast_exp2(m_run - cm);
         l_run *= rescale;
-        acc *= rescale;
 #pragma unroll
-        for (int j = 0; j < kChunk; ++j) {
+        for (int e = 0; e < 8; ++e) acc[e] *= rescale;
+#pragma unroll
+        for (int j = 0; j < kCombChunk; ++j) {
           const bool live = s0 + j < splits && mlv[j].x != -INFINITY;
           const float wgt = live ? hx::fast_exp2(mlv[j].x - cm) * mlv[j].y : 0.f;  // partial stores o / l
           l_run += wgt;
-          acc += wgt * ov[j];
+          const uint32_t w4[4] = {ov[j].x, ov[j].y, ov[j].z, ov[j].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            acc[2 * e] += wgt * hx::Elem<__bf16>::lo(w4[e]);
+            acc[2 * e + 1] += wgt * hx::Elem<__bf16>::hi(w4[e]);
+          }
         }
         m_run = cm;
       }
     }
-    const float val = l_run > 0.f ? acc / l_run : 0.f;
-    reinterpret_cast<uint16_t*>(a.out)[(int64_t)q0 * a.o_row + (int64_t)qh * a.o_head + d] = E::bits(val);
-    if (a.lse && d == 0)
-      a.lse[(int64_t)qh * a.total_q + q0] = l_run > 0.f ? (m_run + log2f(l_run)) * kLn2 : -INFINITY;
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    const int row = q0 + r;
+    const uint4 u = make_uint4(hx::pack2_round<T>(acc[0] * inv, acc[1] * inv), hx::pack2_round<T>(acc[2] * inv, acc[3] * inv),
+                               hx::pack2_round<T>(acc[4] * inv, acc[5] * inv), hx::pack2_round<T>(acc[6] * inv, acc[7] * inv));
+    T* orow = reinterpret_cast<T*>(a.out) + (int64_t)row * a.o_row + (int64_t)qh * a.o_head + 8 * ch;
+    if (a.o_row % 8 == 0 && a.o_head % 8 == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0) {
+      *reinterpret_cast<uint4*>(orow) = u;
+    } else {
+      uint2* o2 = reinterpret_cast<uint2*>(orow);  // rows are 8-byte aligned (checked on the host)
+      o2[0] = make_uint2(u.x, u.y);
+      o2[1] = make_uint2(u.z, u.w);
+    }
+    if (a.lse && ch == 0)
+      a.lse[(int64_t)qh * a.total_q + row] = l_run > 0.f ? (m_run + log2f(l_run)) * kLn2 : -INFINITY;
   }
 }
 
@@ -708,14 +860,17 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   const int q0 = __builtin_amdgcn_readfirstlane(si.x), n = __builtin_amdgcn_readfirstlane(si.y);
   const int L = __builtin_amdgcn_readfirstlane(si.z), kvb = __builtin_amdgcn_readfirstlane(si.w);
   const int off = L - n;  // key position of query row 0
-  const int wg_row_end = min(n, row0 + 32 * (8 / Gw));
-
-  int klo = 0;
-  if (a.win_left >= 0) klo = max(0, off + row0 - a.win_left);
-  int khi = L - 1;
-  if (a.win_right >= 0) khi = min(khi, off + wg_row_end - 1 + a.win_right);
-  const int t_begin = klo / kTile;
-  const int t_end = khi >= klo ? khi / kTile + 1 : t_begin;
+  // Split sp of S covers an equal share of the block's key tiles (S = 1: all of them).
+  const int sp = __builtin_amdgcn_readfirstlane(it.w & 0xffff);
+  const int S = __builtin_amdgcn_readfirstlane((it.w >> 16) + 1);
+  int t_begin, t_end;
+  chunk_tiles(n, L, row0, 256 / Gw, a.win_left, a.win_right, &t_begin, &t_end);
+  const int khi = t_end > t_begin ? min(L - 1, t_end * kTile - 1) : -1;  // last key the pages cover
+  if (S > 1) {
+    const int span = (t_end - t_begin + S - 1) / S;
+    t_begin = min(t_end, t_begin + sp * span);
+    t_end = min(t_end, t_begin + span);
+  }
 
   const int wr0 = row0 + 32 * (w / Gw);
   const int qh = g * G + hquad * Gw + (w % Gw);
@@ -945,13 +1100,30 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   }
 
   // Normalise and store: lane holds dims 16db+4(lane>>4)+0..3 of row 16rb+(lane&15).
+  // A split writes its partial (m in log2 units, l, o / l) to the row's slot instead.
+  const int64_t slot0 = S > 1 ? a.dec_cap + a.pf_base[item] + sp : 0;
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
     float l = l_run[rb];
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
     const int rr = wr0 + 16 * rb + (lane & 15);
-    if (rr < n) {
+    if (rr < n && S > 1) {
+      const int64_t slot = slot0 + (int64_t)(rr - row0) * S;
+      if (slot < a.slot_cap) {
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        uint16_t* prow = a.part_o + (slot * a.hq + qh) * kD;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+          const int d0 = 16 * db + 4 * (lane >> 4);
+          const uint2 u = make_uint2(hx::pack2_round<__bf16>(oacc[db][rb][0] * inv, oacc[db][rb][1] * inv),
+                                     hx::pack2_round<__bf16>(oacc[db][rb][2] * inv, oacc[db][rb][3] * inv));
+          *reinterpret_cast<uint2*>(prow + d0) = u;
+        }
+        if ((lane >> 4) == 0)
+          a.part_ml[slot * a.hq + qh] = make_float2(l > 0.f ? m_run[rb] * sl2 : -INFINITY, l);
+      }
+    } else if (rr < n) {
       const float inv = l > 0.f ? 1.f / l : 0.f;
       uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + (int64_t)(q0 + rr) * a.o_row + (int64_t)qh * a.o_head;
 #pragma unroll
@@ -973,12 +1145,13 @@ bool valid_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
 
 template <typename T, int G>
 int launch_run(const RunArgs& a, hipStream_t s) {
+  // The combine merges decode and chunk split partials, so it runs last.
   if (a.grid_dec > 0)
     hipLaunchKernelGGL((decode_kernel<T, G>), dim3((unsigned)(a.grid_dec * a.hkv)), dim3(kThreads), 0, s, a);
-  if (a.grid_comb > 0)
-    hipLaunchKernelGGL((combine_kernel<T, G>), dim3((unsigned)(a.grid_comb * a.hkv)), dim3(kThreads), 0, s, a);
   if (a.grid_pf > 0)
     hipLaunchKernelGGL((chunk_kernel<T, G>), dim3((unsigned)(a.grid_pf * a.hkv)), dim3(kChunkThreads), 0, s, a);
+  if (a.grid_comb > 0)
+    hipLaunchKernelGGL((combine_kernel<T, G>), dim3((unsigned)(a.grid_comb * a.hkv)), dim3(kThreads), 0, s, a);
   return hx::status_from_hip(hipGetLastError());
 }
 
@@ -1017,25 +1190,43 @@ int hx_varlen_attn_count_items(const int32_t* q_lens, const int32_t* k_lens, int
                                int32_t window_left, int32_t window_right,
                                int32_t* decode_items, int32_t* prefill_items,
                                int32_t* combine_seqs) {
-  (void)window_right;
   if (batch < 0 || n_q_heads < 1 || n_kv_heads < 1 || n_q_heads % n_kv_heads) return HX_E_INVALID_ARG;
   if (batch > 0 && (!q_lens || !k_lens)) return HX_E_INVALID_ARG;
   if (!decode_items || !prefill_items || !combine_seqs) return HX_E_INVALID_ARG;
   const Geometry geo = geometry(n_q_heads, n_kv_heads);
-  int64_t nd = 0, np = 0, nc = 0;
+  // Same two passes as plan_kernel: chunk items and tiles unsplit, then the split.
+  int64_t items0 = 0, tiles0 = 0;
   for (int b = 0; b < batch; ++b) {
     const int n = q_lens[b], L = k_lens[b];
     if (n < 0 || L < 0) return HX_E_INVALID_ARG;
+    if (n < 2) continue;
+    for (int row0 = 0; row0 < n; row0 += geo.rows_per_item) {
+      int tb, te;
+      chunk_tiles(n, L, row0, geo.rows_per_item, window_left, window_right, &tb, &te);
+      tiles0 += (int64_t)(te - tb) * geo.head_quads;
+      items0 += geo.head_quads;
+    }
+  }
+  const int split_tiles = chunk_split_tiles(tiles0, items0, n_kv_heads);
+  int64_t nd = 0, np = 0, nc = 0;
+  for (int b = 0; b < batch; ++b) {
+    const int n = q_lens[b], L = k_lens[b];
     if (n == 1) {
       int first, count;
       decode_splits(L, window_left, &first, &count);
       nd += count;
       nc += count > 1;
     } else if (n >= 2) {
-      np += ceil_div(n, geo.rows_per_item) * geo.head_quads;
+      for (int row0 = 0; row0 < n; row0 += geo.rows_per_item) {
+        int tb, te;
+        chunk_tiles(n, L, row0, geo.rows_per_item, window_left, window_right, &tb, &te);
+        const int S = chunk_split_count(te - tb, split_tiles);
+        np += (int64_t)S * geo.head_quads;
+        if (S > 1) nc += ceil_div(n - row0 < geo.rows_per_item ? n - row0 : geo.rows_per_item, kCombRows);
+      }
     }
   }
-  if (nd > INT32_MAX || np > INT32_MAX) return HX_E_INVALID_ARG;
+  if (nd > INT32_MAX || np > INT32_MAX || nc > INT32_MAX) return HX_E_INVALID_ARG;
   *decode_items = (int32_t)nd;
   *prefill_items = (int32_t)np;
   *combine_seqs = (int32_t)nc;
@@ -1069,9 +1260,12 @@ int hx_varlen_attn_plan(const int32_t* cu_seq_q, const int32_t* cu_seq_k,
   a.dec_items = reinterpret_cast<int4*>(ws + l.dec_items);
   a.comb_seqs = reinterpret_cast<int4*>(ws + l.comb_seqs);
   a.pf_items = reinterpret_cast<int4*>(ws + l.pf_items);
+  a.pf_base = reinterpret_cast<int32_t*>(ws + l.pf_base);
   a.total_k_rows = total_k_rows;
   a.max_dec = l.max_dec;
   a.max_pf = l.max_pf;
+  a.max_comb = l.max_comb;
+  a.cslot_cap = l.cslot_cap;
   a.batch = batch;
   a.total_q = total_q;
   a.max_q = max_q;
@@ -1148,8 +1342,11 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
   a.dec_items = reinterpret_cast<const int4*>(ws + l.dec_items);
   a.comb_seqs = reinterpret_cast<const int4*>(ws + l.comb_seqs);
   a.pf_items = reinterpret_cast<const int4*>(ws + l.pf_items);
+  a.pf_base = reinterpret_cast<const int32_t*>(ws + l.pf_base);
   a.part_ml = reinterpret_cast<float2*>(ws + l.part_ml);
   a.part_o = reinterpret_cast<uint16_t*>(ws + l.part_o);
+  a.dec_cap = l.max_dec;
+  a.slot_cap = l.max_dec + l.cslot_cap;
   a.q_row = q_row_stride;
   a.q_head = q_head_stride;
   a.kv_row = kv_row_stride;
@@ -1174,7 +1371,7 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
   };
   a.grid_dec = clamp_hint(decode_items_hint, l.max_dec);
   a.grid_pf = max_q >= 2 ? clamp_hint(prefill_items_hint, l.max_pf) : 0;
-  a.grid_comb = clamp_hint(combine_seqs_hint, batch);
+  a.grid_comb = clamp_hint(combine_seqs_hint, l.max_comb);
   if ((int64_t)a.grid_dec * n_kv_heads > INT32_MAX || (int64_t)a.grid_pf * n_kv_heads > INT32_MAX)
     return HX_E_INVALID_ARG;
   a.k_new = nullptr;

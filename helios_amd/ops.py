@@ -423,12 +423,13 @@ class VarlenAttnPlan:
         scale: float | None = None,
         out: torch.Tensor | None = None,
         return_lse: bool = False,
-        phases: tuple[str, ...] = ("decode", "combine", "chunk"),
+        phases: tuple[str, ...] = ("decode", "chunk", "combine"),
         append: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
     ) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
         """Attention for one layer. ``phases`` launches a subset of the three kernels
-        (decode splits, split combine, chunk rows); a full result needs all three, in
-        that order, into the same ``out``. Profilers use it to time each kernel.
+        (decode splits, chunk rows, split combine); a full result needs all three, with
+        the combine after the other two (the launch order within one call), into the
+        same ``out``. Profilers use it to time each kernel.
 
         ``append=(k_new, v_new, write_slots)`` first writes the tick's new K/V rows
         into the pool (index_copy_ semantics, as ``kv_append``) in the same call: decode

@@ -46,18 +46,41 @@ def test_workspace_bytes_supported_shapes():
 
 
 def _expected_counts(w: synth.Workload, window=(-1, 0)):
+    """Work items from the closed forms: decode rows split keys in 256s; chunk rows go in
+    blocks of rows_per_item, and when the unsplit blocks launch fewer than 512 workgroups
+    each block's 64-key tiles are cut into splits of at least max(8, ceil(tiles * Hkv /
+    512)) tiles, every split row adding one combine record."""
     nd = nc = npf = 0
     G = w.n_q_heads // w.n_kv_heads
     gw = min(G, 4)
+    quads = G // gw
     rows_per_item = 64 * (4 // gw)
+
+    def tiles(n, L, row0):
+        off = L - n
+        row_end = min(n, row0 + rows_per_item)
+        klo = 0 if window[0] < 0 else max(0, off + row0 - window[0])
+        khi = L - 1 if window[1] < 0 else min(L - 1, off + row_end - 1 + window[1])
+        return (khi // 64 + 1 - klo // 64) if khi >= klo else 0
+
+    blocks = [(n, L, r0) for n, L in zip(w.q_lens, w.k_lens) if n > 1 for r0 in range(0, n, rows_per_item)]
+    items0 = len(blocks) * quads
+    tiles0 = sum(tiles(*blk) for blk in blocks) * quads
+    split = 0
+    if items0 and items0 * w.n_kv_heads < 512:
+        split = max(8, -(-tiles0 * w.n_kv_heads // 512))
     for n, L in zip(w.q_lens, w.k_lens):
         if n == 1:
             lo = 0 if window[0] < 0 else max(0, L - 1 - window[0])
             splits = (L - 1) // 256 - lo // 256 + 1 if L > 0 else 1
             nd += splits
             nc += splits > 1
-        elif n > 1:
-            npf += math.ceil(n / rows_per_item) * (G // gw)
+    for n, L, r0 in blocks:
+        t = tiles(n, L, r0)
+        s = 1 if not split or t <= split else min(64, -(-t // split))
+        npf += s * quads
+        if s > 1:
+            nc += -(-min(rows_per_item, n - r0) // 8)  # combine records of up to 8 rows
     return nd, npf, nc
 
 
