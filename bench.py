@@ -411,8 +411,9 @@ def full_tick_leg(device, ticks: int = 4, seed: int = 5):
     1152 packed tokens, one logit row per sequence. Every tick is rolled back with
     truncate() so each timed tick is the same. Reports tokens/s of the whole tick and
     the attention step's share (q/k norm + RoPE + KV append + paged attention), for
-    this build's path (metadata kernel, fused norm/RoPE/append) and for the reference's
-    sequence on the same kernels (host metadata lists, torch norm/RoPE, attend)."""
+    this build's path (metadata kernel, fused norm/RoPE/append, shared-prefix cascade)
+    and for the reference's sequence on the same kernels (host metadata lists, torch
+    norm/RoPE, attend, every row reading its own prefix pages)."""
     import numpy as np
     import torch
 
@@ -459,7 +460,7 @@ def full_tick_leg(device, ticks: int = 4, seed: int = 5):
                        "sharing <=16 pages of a 4096-token prefix + one 1024-token chunk after "
                        "that prefix; 1152 packed tokens", "tokens": tokens}
     for name, device_meta, fused in (("this_build", True, True), ("reference_sequence", False, False)):
-        batch = PackedBatchCache(caches, device_metadata=device_meta)
+        batch = PackedBatchCache(caches, device_metadata=device_meta, prefix_cascade=device_meta)
         for _ in range(2):
             tick(batch, fused)
         torch.cuda.synchronize()

@@ -122,6 +122,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_void_p, _c_void_p, _i64,
          _c_void_p, _c_void_p],
     ),
+    "hx_attn_merge": (
+        ctypes.c_int,
+        [_c_void_p, _i64, _i64, _c_void_p, _i64,
+         _c_void_p, _i64, _i64, _c_void_p, _i64,
+         _c_void_p, _i64, _i32, _i32, _i32, _c_void_p],
+    ),
     "hx_tick_metadata": (
         ctypes.c_int,
         [_c_void_p, _i32, _i32, _i32,

@@ -174,6 +174,36 @@ def qk_norm_rope_append(
     return out
 
 
+# ------------------------------------------------------------ attention merge
+def attn_merge(out: torch.Tensor, lse_out: torch.Tensor, o_a: torch.Tensor, lse_a: torch.Tensor,
+               rows: torch.Tensor) -> None:
+    """In place: merge attention result ``(o_a[j], lse_a[:, j])`` over one key set into
+    ``(out[rows[j]], lse_out[:, rows[j]])`` over a disjoint one (log-sum-exp weights).
+
+    ``out`` ``[T, H, 128]`` and ``o_a`` ``[n, H, 128]`` (contiguous last dim), ``lse_out``
+    fp32 ``[H, T]``, ``lse_a`` fp32 ``[H, n]``, ``rows`` int64 ``[n]``."""
+    device = _require_gpu(out, lse_out, o_a, lse_a, rows)
+    if out.ndim != 3 or o_a.ndim != 3 or out.shape[1:] != o_a.shape[1:] or out.dtype != o_a.dtype:
+        raise ValueError("out and o_a must be [rows, heads, head_dim] of one dtype.")
+    if out.stride(2) != 1 or o_a.stride(2) != 1:
+        raise ValueError("out and o_a need a contiguous head_dim.")
+    n, heads = o_a.shape[0], o_a.shape[1]
+    for name, t, cols in (("lse_out", lse_out, out.shape[0]), ("lse_a", lse_a, n)):
+        if t.dtype != torch.float32 or tuple(t.shape) != (heads, cols) or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous float32 [heads, rows].")
+    if rows.dtype != torch.int64 or rows.numel() != n or not rows.is_contiguous():
+        raise ValueError("rows must be contiguous int64 [n].")
+    dtype = _SUPPORTED.get(out.dtype)
+    if dtype is None:
+        raise ValueError("attention outputs must be bfloat16 or float16.")
+    code = _capi.lib().hx_attn_merge(
+        out.data_ptr(), out.stride(0), out.stride(1), lse_out.data_ptr(), out.shape[0],
+        o_a.data_ptr(), o_a.stride(0), o_a.stride(1), lse_a.data_ptr(), n,
+        rows.data_ptr(), n, heads, o_a.shape[2], dtype, _stream_ptr(device),
+    )
+    _capi.check(code, "hx_attn_merge")
+
+
 # --------------------------------------------------------------- tick metadata
 def tick_metadata(
     seq: torch.Tensor,

@@ -278,6 +278,23 @@ int hx_qk_norm_rope_append(const void* q, int64_t q_row_stride, int64_t q_head_s
                            void* k_pool, void* v_pool, int64_t pool_rows,
                            const int64_t* write_slots, void* stream);
 
+/*
+ * Merge of two attention results over disjoint key sets of the same query rows (the
+ * shared-prefix split of PagedBatchCache.attend; no counterpart in the reference, whose
+ * varlen_attn reads every sequence's prefix pages itself). For j < n_rows and head h,
+ * with r = rows[j] and m = max(lse_a, lse_out):
+ *   out[r][h]     = (o_a[j][h] e^(lse_a - m) + out[r][h] e^(lse_out - m)) / (sum of weights)
+ *   lse_out[h][r] = m + log(sum of weights)
+ * lse arrays are fp32 [n_heads, total] (the layout of hx_varlen_attn's lse). Rows where
+ * both lse are -inf are left unchanged. head_dim must be 128.
+ */
+int hx_attn_merge(void* out, int64_t out_row_stride, int64_t out_head_stride,
+                  float* lse_out, int64_t total_out,
+                  const void* o_a, int64_t a_row_stride, int64_t a_head_stride,
+                  const float* lse_a, int64_t total_a,
+                  const int64_t* rows, int64_t n_rows,
+                  int32_t n_heads, int32_t head_dim, int32_t dtype, void* stream);
+
 int hx_tick_metadata(const int32_t* seq, int32_t batch, int32_t total_q, int32_t n_logits,
                      const int32_t* block_table, int32_t block_table_stride,
                      int32_t page_size,

@@ -1,0 +1,151 @@
+"""Shared-prefix cascade on the GPU: decode rows that share restored prefix pages attend to
+them once per group; outputs match the float64 oracle and the non-cascade path."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helios_amd import ops
+from helios_amd.config import Qwen3Config
+from helios_amd.paged_cache import KVPagePool, PackedBatchCache, PagedBatchCache, PagedKVCache, _PrefixCascade
+from oracle import attention
+from tests.gpu_cases import MAX_ABS, MEAN_ABS, say
+
+pytestmark = pytest.mark.gpu
+
+
+def _pool(device, pages=96, seed=3):
+    config = Qwen3Config(context_length=8192, n_layers=2, dtype=torch.bfloat16)
+    pool = KVPagePool(config, pages, device=device)
+    g = torch.Generator(device=device).manual_seed(seed)
+    for t in pool.keys + pool.values:
+        t.normal_(generator=g)
+    return pool
+
+
+def _shared_caches(pool, cached, prefix_pages=8):
+    """A prefix of `prefix_pages` full pages, then requests that restore min(prefix,
+    their full pages) of it (shared page objects) and own the rest."""
+    prefix = PagedKVCache(pool, 8192)
+    prefix.pages.extend(pool.acquire(prefix_pages))
+    prefix.length = prefix_pages * 256
+    caches = []
+    for n in cached:
+        cache = PagedKVCache(pool, 8192)
+        shared = min(prefix_pages, n // 256)
+        cache.pages.extend(prefix.pages[:shared])
+        cache.pages.extend(pool.acquire(-(-n // 256) - shared))
+        cache.length = n
+        caches.append(cache)
+    return prefix, caches
+
+
+def _oracle(pool, caches, counts, q, layer=0):
+    k = pool.keys[layer].float().cpu().numpy()
+    v = pool.values[layer].float().cpu().numpy()
+    tables = [[p.index for p in c.pages] for c in caches]
+    ends = [c.length + n for c, n in zip(caches, counts)]
+    cu = np.concatenate([[0], np.cumsum(counts)])
+    out, _ = attention.paged_varlen_attention(q.float().cpu().numpy(), k, v, cu, ends, tables,
+                                              scale=1 / np.sqrt(128))
+    return out
+
+
+def _compare(got, want, what):
+    err = np.abs(got - want)
+    assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (what, err.max(), err.mean())
+
+
+def test_groups_follow_shared_pages(device):
+    say("cascade groups")
+    pool = _pool(device)
+    _, caches = _shared_caches(pool, [300, 2100, 700, 2100, 1600, 40, 999])
+    batch = PagedBatchCache(caches)
+    groups = _PrefixCascade.groups(batch, [1] * len(caches))
+    # shared full pages: 300 -> 1, 2100 -> 8, 700 -> 2, 2100 -> 8, 1600 -> 6, 40 -> 0, 999 -> 3
+    by_p = {p: rows for _, p, rows in groups}
+    assert by_p[8] == [1, 3]
+    assert all(len(rows) >= 2 for rows in by_p.values())
+    assert 5 not in [r for rows in by_p.values() for r in rows]
+
+
+@pytest.mark.parametrize("counts_kind", ["decode", "mixed"])
+def test_cascade_matches_oracle_and_plain_path(device, counts_kind):
+    say("cascade", counts_kind)
+    cached = [2100, 2300, 300, 2100, 1700, 520, 2048, 900, 2800]
+    counts = [1] * len(cached)
+    if counts_kind == "mixed":
+        counts[2] = 130  # a chunk row block next to the decode rows
+    outs = []
+    for cascade in (True, False):
+        pool = _pool(device)
+        _, caches = _shared_caches(pool, cached)
+        batch = PackedBatchCache(caches, prefix_cascade=cascade)
+        batch.prepare_packed(counts)
+        assert (batch._cascade is not None) == cascade
+        total = sum(counts)
+        g = torch.Generator(device=device).manual_seed(11)
+        q = torch.randn((1, 32, total, 128), generator=g, device=device).to(torch.bfloat16)
+        k = torch.randn((1, 8, total, 128), generator=g, device=device).to(torch.bfloat16)
+        v = torch.randn((1, 8, total, 128), generator=g, device=device).to(torch.bfloat16)
+        out = batch.attend(0, q, k, v)
+        torch.cuda.synchronize()
+        want = _oracle(pool, caches, counts, q[0].transpose(0, 1))
+        got = out[0].transpose(0, 1).float().cpu().numpy()
+        _compare(got, want, f"cascade={cascade}")
+        outs.append(got)
+        batch.advance_packed()
+    _compare(outs[0], outs[1], "cascade vs plain")
+
+
+def test_uniform_decode_cascade_over_ticks(device):
+    say("cascade uniform ticks")
+    pool = _pool(device)
+    _, caches = _shared_caches(pool, [2047, 2100, 600, 2300])
+    batch = PagedBatchCache(caches)
+    for tick in range(3):
+        batch.prepare(1)
+        assert batch._cascade is not None
+        g = torch.Generator(device=device).manual_seed(tick)
+        q = torch.randn((4, 32, 1, 128), generator=g, device=device).to(torch.bfloat16)
+        k = torch.randn((4, 8, 1, 128), generator=g, device=device).to(torch.bfloat16)
+        v = torch.randn((4, 8, 1, 128), generator=g, device=device).to(torch.bfloat16)
+        out = batch.attend(1, q, k, v)
+        torch.cuda.synchronize()
+        want = _oracle(pool, caches, [1] * 4, q[:, :, 0], layer=1)
+        _compare(out[:, :, 0].float().cpu().numpy(), want, f"tick {tick}")
+        batch.advance(1)
+
+
+def test_attn_merge_matches_joint_softmax(device):
+    say("attn merge")
+    g = torch.Generator(device="cpu").manual_seed(0)
+    rows, heads, d, ka, kb = 5, 4, 128, 37, 53
+    q = torch.randn(rows, heads, d, generator=g)
+    keys = torch.randn(ka + kb, heads, d, generator=g)
+    vals = torch.randn(ka + kb, heads, d, generator=g)
+
+    def part(lo, hi):
+        s = torch.einsum("rhd,khd->rhk", q, keys[lo:hi]) / np.sqrt(d)
+        lse = torch.logsumexp(s, dim=-1)
+        o = torch.einsum("rhk,khd->rhd", torch.softmax(s, dim=-1), vals[lo:hi])
+        return o, lse
+
+    o_a, lse_a = part(0, ka)
+    o_b, lse_b = part(ka, ka + kb)
+    o_all, lse_all = part(0, ka + kb)
+    total = rows + 3  # o_b rows sit among others at rows 3..7
+    out = torch.zeros(total, heads, d)
+    out[3:] = o_b
+    lse_out = torch.full((heads, total), -float("inf"))
+    lse_out[:, 3:] = lse_b.t()
+    out_d = out.to(torch.bfloat16).to(device)
+    lse_d = lse_out.to(device).contiguous()
+    ops.attn_merge(out_d, lse_d, o_a.to(torch.bfloat16).to(device), lse_a.t().contiguous().to(device),
+                   torch.arange(3, total, device=device))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out_d[3:].float().cpu(), o_all, atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(lse_d[:, 3:].cpu(), lse_all.t(), atol=1e-4, rtol=1e-4)
+    assert not out_d[:3].float().any()
