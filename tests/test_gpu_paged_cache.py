@@ -124,3 +124,48 @@ def test_restore_by_copy_gives_private_identical_pages(device):
     del snap, src, shared, private, batch, b, cache
     gc.collect()
     assert pool.free_pages == pool.num_pages
+
+
+def test_full_hit_restore_recomputes_only_the_last_token(device):
+    """Copy-on-write restore of a prompt the prefix cache covers completely: the pages
+    stay shared except the last, which is a private bit-copy the request can truncate
+    into and rewrite; the shared page is never written."""
+    say("restore private tail")
+    cfg = config(n_layers=2)
+    pool = KVPagePool(cfg, 12, device=device)
+    src = PagedKVCache(pool, 2048)
+    fill = PagedBatchCache([src])
+    fill.prepare(512)
+    g = torch.Generator(device=device).manual_seed(5)
+    for layer in range(cfg.n_layers):
+        q = torch.randn(1, cfg.n_heads, 512, cfg.head_dim, generator=g, device=device).to(cfg.dtype)
+        k = torch.randn(1, cfg.n_kv_heads, 512, cfg.head_dim, generator=g, device=device).to(cfg.dtype)
+        fill.attend(layer, q, k, torch.randn_like(k))
+    fill.advance(512)
+    snaps = [src.snapshot_block(0, 256), src.snapshot_block(256, 512)]
+    before = [t.clone() for t in pool.keys + pool.values]
+    req = PagedKVCache(pool, 2048)
+    req.restore_blocks(snaps, private_tail=True)
+    assert req.length == 512
+    assert req.pages[0] is snaps[0].pages[0]                  # shared
+    assert req.pages[1].index != snaps[1].pages[0].index      # private copy
+    torch.cuda.synchronize()
+    src_i, dst_i = snaps[1].pages[0].index, req.pages[1].index
+    for store in (pool.keys, pool.values):
+        for layer in range(cfg.n_layers):
+            assert torch.equal(store[layer][src_i].view(torch.int16), store[layer][dst_i].view(torch.int16))
+    # recompute the last prompt token into the private page
+    req.truncate(511)
+    tick = PagedBatchCache([req])
+    tick.prepare(1)
+    assert tick.write_slots.tolist() == [dst_i * 256 + 255]
+    for layer in range(cfg.n_layers):
+        q = torch.randn(1, cfg.n_heads, 1, cfg.head_dim, generator=g, device=device).to(cfg.dtype)
+        k = torch.randn(1, cfg.n_kv_heads, 1, cfg.head_dim, generator=g, device=device).to(cfg.dtype)
+        tick.attend(layer, q, k, torch.randn_like(k))
+    tick.advance(1)
+    torch.cuda.synchronize()
+    after = pool.keys + pool.values
+    for t0, t1 in zip(before, after):
+        assert torch.equal(t0[src_i].view(torch.int16), t1[src_i].view(torch.int16))  # shared page untouched
+        assert torch.equal(t0[snaps[0].pages[0].index].view(torch.int16), t1[snaps[0].pages[0].index].view(torch.int16))
