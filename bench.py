@@ -61,10 +61,23 @@ def parse_args():
     p.add_argument("--no-packed-tick", action="store_true")
     p.add_argument("--full-tick", action=argparse.BooleanOptionalAction, default=True,
                    help="full random-init Qwen3-4B tick (128 decoders + a 1024-token chunk)")
+    p.add_argument("--only", default=None,
+                   help="comma-separated side legs to run after the decode leg (packed_tick, "
+                        "long_context, tick_metadata, norm_rope_append, greedy_heads, full_tick); "
+                        "no CPU baseline. For profiling one leg.")
     p.add_argument("--pmc-pass", action="store_true",
                    help="short run for rocprofv3 counter collection: a calibration page "
                         "copy of known size, then a few decode steps")
-    return p.parse_args()
+    args = p.parse_args()
+    if args.only is not None:
+        args.only = [name.strip() for name in args.only.split(",") if name.strip()]
+        unknown = [name for name in args.only if name not in SIDE_LEGS]
+        if unknown:
+            p.error(f"unknown legs {unknown}; choose from {list(SIDE_LEGS)}")
+    return args
+
+
+SIDE_LEGS = ("packed_tick", "long_context", "tick_metadata", "norm_rope_append", "greedy_heads", "full_tick")
 
 
 class DecodeBench:
@@ -326,6 +339,39 @@ def tick_metadata_leg(device, ticks: int = 20):
     return out
 
 
+def _graph_time_us(fn, reps: int, per_graph: int = 10) -> tuple[float, float]:
+    """(device µs per call, host µs per eager call) of ``fn``. Device time: ``per_graph``
+    calls captured in a HIP graph (on a default-priority side stream) and replayed, so
+    host launch overhead does not leave the GPU idle between them."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(per_graph):
+            fn()
+    graph.replay()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in ev:
+        a.record()
+        graph.replay()
+        b.record()
+    torch.cuda.synchronize()
+    device_us = statistics.median(a.elapsed_time(b) for a, b in ev) * 1e3 / per_graph
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    t1 = time.perf_counter()
+    torch.cuda.synchronize()
+    del graph
+    return round(device_us, 2), round((t1 - t0) / reps * 1e6, 1)
+
+
 def norm_rope_leg(device, reps: int = 50):
     """q_norm/k_norm + RoPE + KV append of one layer's new rows: the reference's torch op
     sequence (layers.py:146-160, then _write's two index_copy_) vs the fused kernel, for
@@ -367,35 +413,7 @@ def norm_rope_leg(device, reps: int = 50):
 
         res = {}
         for name, fn in (("reference_ops", reference), ("fused_kernel", fused)):
-            # Device time: 10 calls captured in a HIP graph and replayed, so host launch
-            # overhead does not leave the GPU idle between them.
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                for _ in range(3):
-                    fn()
-            torch.cuda.current_stream().wait_stream(side)
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                for _ in range(10):
-                    fn()
-            graph.replay()
-            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-            for a, b in ev:
-                a.record()
-                graph.replay()
-                b.record()
-            torch.cuda.synchronize()
-            res[f"{name}_gpu_us"] = round(statistics.median(a.elapsed_time(b) for a, b in ev) * 1e3 / 10, 2)
-            # Host time of one eager call (what the scheduler thread spends launching).
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(reps):
-                fn()
-            t1 = time.perf_counter()
-            torch.cuda.synchronize()
-            res[f"{name}_host_us"] = round((t1 - t0) / reps * 1e6, 1)
-            del graph
+            res[f"{name}_gpu_us"], res[f"{name}_host_us"] = _graph_time_us(fn, reps)
         nbytes = rows * (hq + 2 * hkv) * d * 2 * 2 + rows * 2 * d * 4 * 2
         res["fused_gbs"] = round(nbytes / (res["fused_kernel_gpu_us"] * 1e-6) / 1e9, 1)
         out[f"rows_{rows}"] = res
@@ -404,16 +422,58 @@ def norm_rope_leg(device, reps: int = 50):
     return out
 
 
+def greedy_heads_leg(device, reps: int = 30):
+    """The tick's greedy heads at the Qwen3-4B shape (hidden 2560, tied vocab 151936):
+    the reference's sequence (index_select, RMSNorm, Linear to bf16 logits, argmax;
+    model.py:108-110, engine.py:470-473) vs the fused final-norm / logits / argmax
+    kernels, for 1, 64 and 129 logit rows of a 1152-row tick."""
+    import torch
+
+    from helios_amd import ops
+    from oracle import dense_torch
+
+    hidden, vocab, rows = 2560, 151936, 1152
+    g = torch.Generator(device=device).manual_seed(7)
+    x = torch.randn((rows, hidden), generator=g, device=device).to(torch.bfloat16)
+    emb = (0.02 * torch.randn((vocab, hidden), generator=g, device=device)).to(torch.bfloat16)
+    w = torch.ones(hidden, device=device)
+    weight_bytes = vocab * hidden * 2
+    out = {"weight_bytes": weight_bytes}
+    for n in (1, 64, 129):
+        idx = torch.arange(rows - n, rows, device=device)
+
+        def reference():
+            h = dense_torch.rms_norm(x.index_select(0, idx), w, 1e-6)
+            return torch.nn.functional.linear(h, emb).argmax(dim=-1)
+
+        def fused():
+            return ops.final_norm_logits_argmax(x, idx, w, emb, 1e-6).token_ids
+
+        same = bool(torch.equal(reference(), fused()))
+        res = {"same_ids": same}
+        for name, fn in (("reference_ops", reference), ("fused_kernels", fused)):
+            res[f"{name}_gpu_us"], res[f"{name}_host_us"] = _graph_time_us(fn, reps)
+        t = res["fused_kernels_gpu_us"] * 1e-6
+        res["fused_weight_gbs"] = round(weight_bytes / t / 1e9, 1)
+        res["fused_hbm_frac"] = round(weight_bytes / t / 1e9 / HBM_PEAK_GBS, 4)
+        res["fused_tflops"] = round(2.0 * n * hidden * vocab / t / 1e12, 1)
+        out[f"rows_{n}"] = res
+    del emb
+    torch.cuda.empty_cache()
+    return out
+
+
 def full_tick_leg(device, ticks: int = 4, seed: int = 5):
     """Full random-init Qwen3-4B forward of one continuous-batching tick: 128 decoders
     (contexts uniform in 1024-8192, each sharing up to 16 pages of a 4096-token system
     prefix) plus one 1024-token prefill chunk that also starts from the shared prefix;
-    1152 packed tokens, one logit row per sequence. Every tick is rolled back with
-    truncate() so each timed tick is the same. Reports tokens/s of the whole tick and
-    the attention step's share (q/k norm + RoPE + KV append + paged attention), for
-    this build's path (metadata kernel, fused norm/RoPE/append, shared-prefix cascade)
-    and for the reference's sequence on the same kernels (host metadata lists, torch
-    norm/RoPE, attend, every row reading its own prefix pages)."""
+    1152 packed tokens, one logit row per sequence, greedy token ids out. Every tick is
+    rolled back with truncate() so each timed tick is the same. Reports tokens/s of the
+    whole tick and the attention step's share (q/k norm + RoPE + KV append + paged
+    attention), for this build's path (metadata kernel, fused norm/RoPE/append,
+    shared-prefix cascade, fused final-norm/logits/argmax) and for the reference's
+    sequence on the same attention kernels (host metadata lists, torch norm/RoPE,
+    attend, every row reading its own prefix pages, bf16 logits then argmax)."""
     import numpy as np
     import torch
 
@@ -451,14 +511,15 @@ def full_tick_leg(device, ticks: int = 4, seed: int = 5):
 
     def tick(batch, fused, events=None):
         batch.prepare_packed(counts)
-        logits = model.forward_packed(input_ids, batch, fused_rope=fused, attention_events=events)
+        ids = model.forward_packed(input_ids, batch, fused_rope=fused, attention_events=events, greedy=True)
         for cache, n in zip(caches, lengths):
             cache.truncate(n)
-        return logits
+        return ids
 
     res = {"workload": "Qwen3-4B random-init bf16, 36 layers: 128 decoders ctx U[1024,8192] "
                        "sharing <=16 pages of a 4096-token prefix + one 1024-token chunk after "
                        "that prefix; 1152 packed tokens", "tokens": tokens}
+    picks = {}
     for name, device_meta, fused in (("this_build", True, True), ("reference_sequence", False, False)):
         batch = PackedBatchCache(caches, device_metadata=device_meta, prefix_cascade=device_meta)
         for _ in range(2):
@@ -466,7 +527,7 @@ def full_tick_leg(device, ticks: int = 4, seed: int = 5):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(ticks):
-            logits = tick(batch, fused)
+            ids = tick(batch, fused)
         torch.cuda.synchronize()
         sec = (time.perf_counter() - t0) / ticks
         events = []
@@ -480,8 +541,26 @@ def full_tick_leg(device, ticks: int = 4, seed: int = 5):
             "attention_ms_per_tick": round(attn_ms, 3),
             "attention_share": round(attn_ms / (sec * 1e3), 4),
         }
-        assert torch.isfinite(logits.float()).all()
+        assert bool(((ids >= 0) & (ids < config.vocab_size)).all())
+        picks[name] = ids
         del batch
+    # How far this build's greedy picks are from the reference sequence's own maximum:
+    # the two forwards round differently (attention order, fused RoPE, cascade merge), so
+    # near-ties of a random-init model's flat logits may resolve differently.
+    batch = PackedBatchCache(caches, device_metadata=False, prefix_cascade=False)
+    batch.prepare_packed(counts)
+    ref_logits = model.forward_packed(input_ids, batch, fused_rope=False).float()
+    for cache, n in zip(caches, lengths):
+        cache.truncate(n)
+    top = ref_logits.max(dim=-1).values
+    gap = top - ref_logits.gather(1, picks["this_build"].unsqueeze(1))[:, 0]
+    res["greedy_vs_reference_sequence"] = {
+        "same_ids": round(float((picks["this_build"] == picks["reference_sequence"]).float().mean()), 4),
+        "max_logit_gap_of_picks": round(float(gap.max()), 5),
+        "max_logit_mean": round(float(top.mean()), 4),
+        "top2_gap_median": round(float((top - ref_logits.topk(2, dim=-1).values[:, 1]).median()), 5),
+    }
+    del batch
     del model, pool, caches, prefix
     torch.cuda.empty_cache()
     return res
@@ -614,14 +693,23 @@ def main():
     }
     del b, events
     torch.cuda.empty_cache()
-    if not args.no_packed_tick:
-        result["packed_tick"] = packed_tick(device)
-        result["long_context"] = long_context(device)
-        result["tick_metadata"] = tick_metadata_leg(device)
-        result["norm_rope_append"] = norm_rope_leg(device)
-    if args.full_tick:
-        result["full_tick"] = full_tick_leg(device)
-    if not args.no_cpu_baseline:
+    legs = {
+        "packed_tick": packed_tick,
+        "long_context": long_context,
+        "tick_metadata": tick_metadata_leg,
+        "norm_rope_append": norm_rope_leg,
+        "greedy_heads": greedy_heads_leg,
+        "full_tick": full_tick_leg,
+    }
+    if args.only is not None:
+        chosen = args.only
+    else:
+        chosen = [] if args.no_packed_tick else list(legs)[:5]
+        if args.full_tick:
+            chosen.append("full_tick")
+    for name in chosen:
+        result[name] = legs[name](device)
+    if args.only is None and not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)
 

@@ -136,6 +136,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_void_p, _c_void_p, _c_void_p,
          _c_void_p],
     ),
+    "hx_logits_workspace_bytes": (_size, [_i64, _i64, _i32]),
+    "hx_final_norm_logits_argmax": (
+        ctypes.c_int,
+        [_c_void_p, _i64, _i64, _c_void_p,
+         _i64, _c_void_p, _f32,
+         _c_void_p, _i64,
+         _i64, _i32, _i32,
+         _c_void_p, _c_void_p,
+         _c_void_p, _i64,
+         _c_void_p, _size, _c_void_p],
+    ),
 }
 
 _lib: ctypes.CDLL | None = None

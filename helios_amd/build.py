@@ -18,7 +18,7 @@ PACKAGE_DIR = Path(__file__).resolve().parent
 CSRC = PACKAGE_DIR / "csrc"
 INCLUDE = PACKAGE_DIR.parent / "include"
 LIBRARY = PACKAGE_DIR / "libhelios_paged.so"
-SOURCES = ("kv_ops.hip", "paged_attn.hip", "tick_meta.hip", "qk_rope.hip")
+SOURCES = ("kv_ops.hip", "paged_attn.hip", "tick_meta.hip", "qk_rope.hip", "logits.hip")
 ARCH = "gfx950"
 
 

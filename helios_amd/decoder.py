@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import torch
 
+from helios_amd import ops
 from helios_amd.config import Qwen3Config
 from helios_amd.paged_cache import PackedBatchCache
 
@@ -75,9 +76,15 @@ class PagedQwen3Decoder:
 
     @torch.inference_mode()
     def forward_packed(self, input_ids: torch.Tensor, cache: PackedBatchCache, *,
-                       fused_rope: bool = True, attention_events: list | None = None) -> torch.Tensor:
-        """Logits of the tick's logit rows (model.py:92-110). ``attention_events``
-        collects (start, end) CUDA events around each layer's attention step."""
+                       fused_rope: bool = True, attention_events: list | None = None,
+                       greedy: bool = False) -> torch.Tensor:
+        """Logits of the tick's logit rows (model.py:92-110), or with ``greedy`` their
+        argmax token ids (engine.py:470-473). ``attention_events`` collects (start, end)
+        CUDA events around each layer's attention step.
+
+        With ``fused_rope`` (this build's sequence) the greedy ids come from the fused
+        final-norm / logits / argmax kernels and no logits are written; otherwise the
+        reference's logits are computed and ``argmax`` taken."""
         config = self.config
         if input_ids.shape != (1, sum(cache.counts)):
             raise ValueError("Packed input does not match query lengths.")
@@ -112,5 +119,9 @@ class PagedQwen3Decoder:
             gate, up = (h @ layer["gate_up"].t()).chunk(2, dim=-1)
             x = x + (torch.nn.functional.silu(gate) * up) @ layer["down"].t()
         cache.advance_packed()
+        if greedy and fused_rope:
+            return ops.final_norm_logits_argmax(x, cache.logit_indices, self.final_norm, self.embedding,
+                                                eps).token_ids
         x = x.index_select(1, cache.logit_indices)
-        return (_rms_norm(x, self.final_norm, eps).to(config.dtype) @ self.embedding.t())[0]
+        logits = (_rms_norm(x, self.final_norm, eps).to(config.dtype) @ self.embedding.t())[0]
+        return logits.argmax(dim=-1) if greedy else logits

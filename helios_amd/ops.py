@@ -204,6 +204,78 @@ def attn_merge(out: torch.Tensor, lse_out: torch.Tensor, o_a: torch.Tensor, lse_
     _capi.check(code, "hx_attn_merge")
 
 
+# --------------------------------------------------------------- logits and argmax
+class GreedyHeads(NamedTuple):
+    """Result of ``final_norm_logits_argmax``: ``token_ids`` int64 ``[n]`` (-1 for an index
+    outside the hidden rows), ``max_logits`` fp32 ``[n]``, and ``logits`` ``[n, vocab]``
+    in the model dtype when they were asked for (else None)."""
+
+    token_ids: torch.Tensor
+    max_logits: torch.Tensor
+    logits: torch.Tensor | None
+
+
+def final_norm_logits_argmax(
+    hidden_states: torch.Tensor,
+    logit_indices: torch.Tensor,
+    norm_weight: torch.Tensor,
+    embedding: torch.Tensor,
+    eps: float,
+    *,
+    return_logits: bool = False,
+) -> GreedyHeads:
+    """Greedy heads of a packed tick: the final RMSNorm of the logit rows, the tied
+    lm_head and argmax, replacing ``x.index_select(1, logit_indices)``,
+    ``self.output(self.final_norm(x).to(dtype))`` (model.py:108-110) and
+    ``heads.argmax(dim=-1)`` (engine.py:470-473) for greedy sampling.
+
+    ``hidden_states`` ``[T, hidden]`` or ``[1, T, hidden]`` (the last layer's output,
+    contiguous last dim); ``logit_indices`` int64 ``[n]``; ``norm_weight`` fp32
+    ``[hidden]``; ``embedding`` ``[vocab, hidden]`` in the model dtype. Ties go to the
+    smallest vocab index, as in ``torch.argmax``. The logits are computed in fp32,
+    rounded to the model dtype like the Linear's output, and written out only with
+    ``return_logits``.
+    """
+    if hidden_states.ndim == 3:
+        if hidden_states.shape[0] != 1:
+            raise ValueError("hidden_states must be [tokens, hidden] or [1, tokens, hidden].")
+        hidden_states = hidden_states[0]
+    device = _require_gpu(hidden_states, logit_indices, norm_weight, embedding)
+    if hidden_states.ndim != 2 or embedding.ndim != 2 or embedding.shape[1] != hidden_states.shape[1]:
+        raise ValueError("embedding must be [vocab, hidden] matching hidden_states.")
+    if hidden_states.dtype != embedding.dtype:
+        raise ValueError("hidden_states and embedding must share a dtype.")
+    dtype = _SUPPORTED.get(embedding.dtype)
+    if dtype is None:
+        raise ValueError("hidden_states and embedding must be bfloat16 or float16.")
+    if hidden_states.stride(1) != 1 or embedding.stride(1) != 1:
+        raise ValueError("hidden_states and embedding need a contiguous last dimension.")
+    hidden = hidden_states.shape[1]
+    if norm_weight.dtype != torch.float32 or tuple(norm_weight.shape) != (hidden,) or not norm_weight.is_contiguous():
+        raise ValueError("norm_weight must be contiguous float32 [hidden].")
+    if logit_indices.dtype != torch.int64 or logit_indices.ndim != 1 or not logit_indices.is_contiguous():
+        raise ValueError("logit_indices must be contiguous int64 [n].")
+    n, vocab = logit_indices.numel(), embedding.shape[0]
+    token_ids = torch.empty(n, dtype=torch.int64, device=device)
+    max_logits = torch.empty(n, dtype=torch.float32, device=device)
+    logits = torch.empty((n, vocab), dtype=embedding.dtype, device=device) if return_logits else None
+    if n == 0:
+        return GreedyHeads(token_ids, max_logits, logits)
+    lib = _capi.lib()
+    ws_bytes = lib.hx_logits_workspace_bytes(n, vocab, hidden)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    code = lib.hx_final_norm_logits_argmax(
+        hidden_states.data_ptr(), hidden_states.stride(0), hidden_states.shape[0],
+        logit_indices.data_ptr(), n, norm_weight.data_ptr(), float(eps),
+        embedding.data_ptr(), embedding.stride(0), vocab, hidden, dtype,
+        token_ids.data_ptr(), max_logits.data_ptr(),
+        logits.data_ptr() if logits is not None else None, vocab,
+        workspace.data_ptr(), ws_bytes, _stream_ptr(device),
+    )
+    _capi.check(code, "hx_final_norm_logits_argmax")
+    return GreedyHeads(token_ids, max_logits, logits)
+
+
 # --------------------------------------------------------------- tick metadata
 def tick_metadata(
     seq: torch.Tensor,

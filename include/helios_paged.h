@@ -302,6 +302,35 @@ int hx_tick_metadata(const int32_t* seq, int32_t batch, int32_t total_q, int32_t
                      int64_t* positions, int64_t* write_slots, int64_t* logit_indices,
                      void* stream);
 
+/*
+ * Final RMSNorm + lm_head + greedy argmax of the tick's logit rows. Replaces
+ *   x.index_select(1, logit_indices); self.output(self.final_norm(x).to(dtype))
+ * (model.py:108-110; RMSNorm over the hidden size in fp32, layers.py:29-39; the tied
+ * embedding as a bias-free Linear) followed by heads.argmax(dim=-1) on the logits of
+ * greedy rows (engine.py:470-473). For j < n_rows and row x = hidden_states[logit_indices[j]]:
+ *   xn            = round((x * rsqrt(mean(x^2) + eps)) * norm_weight)      (fp32 weight)
+ *   logit[v]      = round(sum_k xn[k] * embedding[v][k])                    (fp32 sum)
+ *   token_ids[j]  = the smallest v with the largest logit[v]
+ *   max_logits[j] = that logit (optional, may be NULL)
+ *   logits        = [n_rows, vocab] rounded logits, row stride logits_row_stride
+ *                   (optional: NULL writes none; the greedy path needs none)
+ * An index outside [0, total_rows) gives token id -1 and max logit NaN. hidden must
+ * be a multiple of 128; strides are in elements and multiples of 8; dtype is
+ * HX_DTYPE_BF16 or HX_DTYPE_FP16 for hidden_states, embedding and logits. Up to 160
+ * rows read the embedding once; more rows read it once per 160. The workspace is
+ * hx_logits_workspace_bytes(n_rows, vocab, hidden) bytes, 256-byte aligned.
+ */
+size_t hx_logits_workspace_bytes(int64_t n_rows, int64_t vocab, int32_t hidden);
+
+int hx_final_norm_logits_argmax(const void* hidden_states, int64_t hidden_row_stride,
+                                int64_t total_rows, const int64_t* logit_indices,
+                                int64_t n_rows, const float* norm_weight, float eps,
+                                const void* embedding, int64_t embedding_row_stride,
+                                int64_t vocab, int32_t hidden, int32_t dtype,
+                                int64_t* token_ids, float* max_logits,
+                                void* logits, int64_t logits_row_stride,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,3 +47,27 @@ def test_packed_forward_matches_reference_sequence(device):
     scale = logits[1].abs().max().item()
     assert (logits[0] - logits[1]).abs().max().item() <= 2e-2 * max(scale, 1.0)
     assert torch.equal(pools[0], pools[1])  # values are appended bit-exactly by both paths
+
+
+def test_greedy_heads_match_logits_argmax(device):
+    say("decoder greedy heads")
+    config = Qwen3Config(vocab_size=1000, context_length=4096, hidden_size=256, n_layers=2,
+                         hidden_dim=512, dtype=torch.bfloat16)
+    model = PagedQwen3Decoder(config, device, seed=2, std=0.05)
+    outs = []
+    for greedy in (False, True):
+        pool = KVPagePool(config, 8, device=device)
+        caches = [PagedKVCache(pool, config.context_length) for _ in range(3)]
+        batch = PackedBatchCache(caches)
+        counts = [5, 130, 1]
+        ids = torch.randint(0, config.vocab_size, (1, sum(counts)),
+                            generator=torch.Generator(device=device).manual_seed(3), device=device)
+        batch.prepare_packed(counts)
+        outs.append(model.forward_packed(ids, batch, greedy=greedy))
+    torch.cuda.synchronize()
+    logits, picks = outs[0].float().cpu(), outs[1].cpu()
+    assert picks.shape == (3,) and picks.dtype == torch.int64
+    top = logits.max(dim=-1).values
+    chosen = logits.gather(1, picks.unsqueeze(1))[:, 0]
+    # the kernel's pick is the argmax up to one bf16 rounding of the logits
+    assert ((top - chosen) <= 2 * 2.0 ** -7 * top.abs() + 1e-4).all()
