@@ -156,11 +156,13 @@ extern "C" int hx_tick_metadata(const int32_t* seq, int32_t batch, int32_t total
 }
 
 // ---------------------------------------------------------------- attention merge
-// Two attention results over disjoint key sets of the same query row, each normalised
-// with its own log-sum-exp, combine exactly into the result over the union:
-//   o = (o_a * e^(lse_a - m) + o_b * e^(lse_b - m)) / (e^(lse_a - m) + e^(lse_b - m)),
-//   lse = m + log(e^(lse_a - m) + e^(lse_b - m)),  m = max(lse_a, lse_b).
-// Row j of (o_a, lse_a) merges into packed row rows[j] of (out, lse_out) in place.
+// Attention results over disjoint key sets of the same query row, each normalised with
+// its own log-sum-exp, combine exactly into the result over the union:
+//   o = (sum_i o_i e^(lse_i - m)) / (sum_i e^(lse_i - m)),  lse = m + log(sum_i e^(lse_i - m)),
+// m = max_i lse_i. Entry j merges its parts (rows of o_a) into packed row rows[j] of
+// (out, lse_out) in place: parts part_idx[part_start[j]] .. part_idx[part_start[j+1]-1],
+// or o_a row j alone when part_start is null. The parts are folded in list order, two
+// at a time as in the formula above with one of them the running result.
 namespace {
 
 template <typename T>
@@ -168,8 +170,9 @@ __global__ __launch_bounds__(256) void merge_kernel(uint16_t* out, int64_t o_row
                                                     float* lse_out, int64_t total_out,
                                                     const uint16_t* oa, int64_t a_row, int64_t a_head,
                                                     const float* lse_a, int64_t total_a,
-                                                    const int64_t* rows, int64_t n_rows, int hq) {
-  // One wave per (row j, head h); lane l owns dims l and l + 64. Every lane reads the old
+                                                    const int64_t* rows, const int32_t* part_start,
+                                                    const int32_t* part_idx, int64_t n_rows, int hq) {
+  // One wave per (entry j, head h); lane l owns dims l and l + 64. Every lane reads the old
   // lse before lane 0 stores the merged one, in program order within the wave.
   const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -178,23 +181,38 @@ __global__ __launch_bounds__(256) void merge_kernel(uint16_t* out, int64_t o_row
   const int h = (int)(item - j * hq);
   const int64_t r = rows[j];
   if (r < 0 || r >= total_out) return;
-  const float la = lse_a[(int64_t)h * total_a + j];
-  float* lb_p = lse_out + (int64_t)h * total_out + r;
-  const float lb = *lb_p;
-  const float m = fmaxf(la, lb);
-  if (m == -INFINITY) return;  // neither side saw a key: keep zeros / -inf
-  const float wa = expf(la - m), wb = expf(lb - m);
-  const float inv = 1.f / (wa + wb);
-  uint16_t* po = out + r * o_row + (int64_t)h * o_head;
-  const uint16_t* pa = oa + j * a_row + (int64_t)h * a_head;
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int d = lane + 64 * k;
-    const float xa = (float)__builtin_bit_cast(T, pa[d]);
-    const float xb = (float)__builtin_bit_cast(T, po[d]);
-    po[d] = __builtin_bit_cast(uint16_t, (T)((xa * wa + xb * wb) * inv));
+  int64_t p0 = j, p1 = j + 1;
+  if (part_start != nullptr) {
+    p0 = part_start[j];
+    p1 = part_start[j + 1];
   }
-  if (lane == 0) *lb_p = m + logf(wa + wb);
+  float* lb_p = lse_out + (int64_t)h * total_out + r;
+  float m = *lb_p;  // the running result is normalised, with log-sum-exp m
+  uint16_t* po = out + r * o_row + (int64_t)h * o_head;
+  float acc[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) acc[k] = (float)__builtin_bit_cast(T, po[lane + 64 * k]);
+  bool changed = false;
+  for (int64_t p = p0; p < p1; ++p) {
+    const int64_t ja = part_start != nullptr ? (int64_t)part_idx[p] : p;
+    if (ja < 0 || ja >= total_a) continue;
+    const float la = lse_a[(int64_t)h * total_a + ja];
+    const float mn = fmaxf(m, la);
+    if (mn == -INFINITY) continue;  // neither side saw a key yet
+    const float wa = expf(la - mn), wb = expf(m - mn);
+    const uint16_t* pa = oa + ja * a_row + (int64_t)h * a_head;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const float xa = (float)__builtin_bit_cast(T, pa[lane + 64 * k]);
+      acc[k] = (xa * wa + acc[k] * wb) / (wa + wb);
+    }
+    m = mn + logf(wa + wb);
+    changed = true;
+  }
+  if (!changed) return;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) po[lane + 64 * k] = __builtin_bit_cast(uint16_t, (T)acc[k]);
+  if (lane == 0) *lb_p = m;
 }
 
 }  // namespace
@@ -203,10 +221,13 @@ extern "C" int hx_attn_merge(void* out, int64_t out_row_stride, int64_t out_head
                              float* lse_out, int64_t total_out,
                              const void* o_a, int64_t a_row_stride, int64_t a_head_stride,
                              const float* lse_a, int64_t total_a,
-                             const int64_t* rows, int64_t n_rows,
-                             int32_t n_heads, int32_t head_dim, int32_t dtype, void* stream) {
+                             const int64_t* rows, const int32_t* part_start, const int32_t* part_idx,
+                             int64_t n_rows, int32_t n_heads, int32_t head_dim, int32_t dtype,
+                             void* stream) {
   if (head_dim != 128 || (dtype != HX_DTYPE_BF16 && dtype != HX_DTYPE_FP16)) return HX_E_UNSUPPORTED;
-  if (n_rows < 0 || n_heads < 1 || total_out < 0 || total_a < n_rows) return HX_E_INVALID_ARG;
+  if (n_rows < 0 || n_heads < 1 || total_out < 0 || total_a < 0) return HX_E_INVALID_ARG;
+  if (part_start == nullptr && total_a < n_rows) return HX_E_INVALID_ARG;
+  if ((part_start == nullptr) != (part_idx == nullptr)) return HX_E_INVALID_ARG;
   if (n_rows == 0) return HX_OK;
   if (!out || !lse_out || !o_a || !lse_a || !rows) return HX_E_INVALID_ARG;
   const int64_t items = n_rows * n_heads;
@@ -217,9 +238,11 @@ extern "C" int hx_attn_merge(void* out, int64_t out_row_stride, int64_t out_head
   const uint16_t* a = static_cast<const uint16_t*>(o_a);
   if (dtype == HX_DTYPE_BF16)
     hipLaunchKernelGGL(merge_kernel<__bf16>, dim3(grid), dim3(256), 0, s, o, out_row_stride, out_head_stride,
-                       lse_out, total_out, a, a_row_stride, a_head_stride, lse_a, total_a, rows, n_rows, n_heads);
+                       lse_out, total_out, a, a_row_stride, a_head_stride, lse_a, total_a, rows, part_start,
+                       part_idx, n_rows, n_heads);
   else
     hipLaunchKernelGGL(merge_kernel<_Float16>, dim3(grid), dim3(256), 0, s, o, out_row_stride, out_head_stride,
-                       lse_out, total_out, a, a_row_stride, a_head_stride, lse_a, total_a, rows, n_rows, n_heads);
+                       lse_out, total_out, a, a_row_stride, a_head_stride, lse_a, total_a, rows, part_start,
+                       part_idx, n_rows, n_heads);
   return hx::status_from_hip(hipGetLastError());
 }

@@ -176,30 +176,49 @@ def qk_norm_rope_append(
 
 # ------------------------------------------------------------ attention merge
 def attn_merge(out: torch.Tensor, lse_out: torch.Tensor, o_a: torch.Tensor, lse_a: torch.Tensor,
-               rows: torch.Tensor) -> None:
-    """In place: merge attention result ``(o_a[j], lse_a[:, j])`` over one key set into
-    ``(out[rows[j]], lse_out[:, rows[j]])`` over a disjoint one (log-sum-exp weights).
+               rows: torch.Tensor, parts: tuple[torch.Tensor, torch.Tensor] | None = None) -> None:
+    """In place: merge attention results over disjoint key sets by log-sum-exp weights.
 
-    ``out`` ``[T, H, 128]`` and ``o_a`` ``[n, H, 128]`` (contiguous last dim), ``lse_out``
-    fp32 ``[H, T]``, ``lse_a`` fp32 ``[H, n]``, ``rows`` int64 ``[n]``."""
+    Without ``parts``, ``(o_a[j], lse_a[:, j])`` merges into ``(out[rows[j]],
+    lse_out[:, rows[j]])``. With ``parts = (part_start, part_idx)`` (int32 ``[n + 1]`` and
+    ``[P]``), entry j merges the o_a rows ``part_idx[part_start[j]:part_start[j + 1]]``
+    into ``out[rows[j]]`` in one pass. ``out`` ``[T, H, 128]`` and ``o_a`` ``[A, H, 128]``
+    (contiguous last dim), ``lse_out`` fp32 ``[H, T]``, ``lse_a`` fp32 ``[H, A]`` (or a
+    column slice of a wider array), ``rows`` int64 ``[n]`` without repeats."""
     device = _require_gpu(out, lse_out, o_a, lse_a, rows)
     if out.ndim != 3 or o_a.ndim != 3 or out.shape[1:] != o_a.shape[1:] or out.dtype != o_a.dtype:
         raise ValueError("out and o_a must be [rows, heads, head_dim] of one dtype.")
     if out.stride(2) != 1 or o_a.stride(2) != 1:
         raise ValueError("out and o_a need a contiguous head_dim.")
-    n, heads = o_a.shape[0], o_a.shape[1]
-    for name, t, cols in (("lse_out", lse_out, out.shape[0]), ("lse_a", lse_a, n)):
-        if t.dtype != torch.float32 or tuple(t.shape) != (heads, cols) or not t.is_contiguous():
-            raise ValueError(f"{name} must be contiguous float32 [heads, rows].")
-    if rows.dtype != torch.int64 or rows.numel() != n or not rows.is_contiguous():
+    n_a, heads = o_a.shape[0], o_a.shape[1]
+    n = rows.numel()
+    if lse_out.dtype != torch.float32 or tuple(lse_out.shape) != (heads, out.shape[0]) or not lse_out.is_contiguous():
+        raise ValueError("lse_out must be contiguous float32 [heads, rows].")
+    # lse_a may be a column slice of a wider [heads, total] array (rows stride(0) apart).
+    if lse_a.dtype != torch.float32 or tuple(lse_a.shape) != (heads, n_a) or (n_a > 0 and lse_a.stride(1) != 1) \
+            or (heads > 1 and lse_a.stride(0) < n_a):
+        raise ValueError("lse_a must be float32 [heads, rows] with contiguous rows.")
+    if rows.dtype != torch.int64 or rows.ndim != 1 or not rows.is_contiguous():
         raise ValueError("rows must be contiguous int64 [n].")
+    start_ptr = idx_ptr = None
+    if parts is None:
+        if n != n_a:
+            raise ValueError("without parts, rows must have one entry per o_a row.")
+    else:
+        part_start, part_idx = parts
+        for name, t in (("part_start", part_start), ("part_idx", part_idx)):
+            if t.dtype != torch.int32 or t.ndim != 1 or not t.is_contiguous() or t.device != device:
+                raise ValueError(f"{name} must be a contiguous int32 vector on the device.")
+        if part_start.numel() != n + 1:
+            raise ValueError("part_start must have one entry per row plus one.")
+        start_ptr, idx_ptr = part_start.data_ptr(), part_idx.data_ptr()
     dtype = _SUPPORTED.get(out.dtype)
     if dtype is None:
         raise ValueError("attention outputs must be bfloat16 or float16.")
     code = _capi.lib().hx_attn_merge(
         out.data_ptr(), out.stride(0), out.stride(1), lse_out.data_ptr(), out.shape[0],
-        o_a.data_ptr(), o_a.stride(0), o_a.stride(1), lse_a.data_ptr(), n,
-        rows.data_ptr(), n, heads, o_a.shape[2], dtype, _stream_ptr(device),
+        o_a.data_ptr(), o_a.stride(0), o_a.stride(1), lse_a.data_ptr(), lse_a.stride(0) if heads > 1 else n_a,
+        rows.data_ptr(), start_ptr, idx_ptr, n, heads, o_a.shape[2], dtype, _stream_ptr(device),
     )
     _capi.check(code, "hx_attn_merge")
 

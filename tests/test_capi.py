@@ -26,7 +26,7 @@ def test_library_exports_every_header_function():
 
 
 def test_abi_version_and_strerror():
-    assert _capi.lib().hx_abi_version() == 1
+    assert _capi.lib().hx_abi_version() == 2
     assert _capi.strerror(0) == "success"
     assert "invalid" in _capi.strerror(_capi.HX_E_INVALID_ARG)
     with pytest.raises(ValueError):

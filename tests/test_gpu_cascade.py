@@ -58,21 +58,31 @@ def _compare(got, want, what):
     assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (what, err.max(), err.mean())
 
 
-def test_groups_follow_shared_pages(device):
-    say("cascade groups")
+@pytest.fixture
+def always_cascade(monkeypatch):
+    """Levels cost nothing, so every shared page range with two rows becomes a level."""
+    monkeypatch.setattr(_PrefixCascade, "US_PER_LEVEL", 0.0)
+    monkeypatch.setattr(_PrefixCascade, "US_PER_BLOCK_PAGE", 0.0)
+
+
+def test_levels_follow_shared_pages(device, always_cascade):
+    say("cascade levels")
     pool = _pool(device)
     _, caches = _shared_caches(pool, [300, 2100, 700, 2100, 1600, 40, 999])
     batch = PagedBatchCache(caches)
-    groups = _PrefixCascade.groups(batch, [1] * len(caches))
-    # shared full pages: 300 -> 1, 2100 -> 8, 700 -> 2, 2100 -> 8, 1600 -> 6, 40 -> 0, 999 -> 3
-    by_p = {p: rows for _, p, rows in groups}
-    assert by_p[8] == [1, 3]
-    assert all(len(rows) >= 2 for rows in by_p.values())
-    assert 5 not in [r for rows in by_p.values() for r in rows]
+    levels = _PrefixCascade.levels(batch, [1] * len(caches))
+    # shared full pages: 300 -> 1, 2100 -> 8, 700 -> 2, 2100 -> 8, 1600 -> 6, 40 -> 0, 999 -> 3;
+    # free levels: one per distinct count, up to three, the deepest covering rows 1 and 3
+    assert len(levels) <= _PrefixCascade.MAX_LEVELS
+    prev = 0
+    for ref, first, end, rows in levels:
+        assert first == prev and end > first and len(rows) >= 2 and 5 not in rows
+        prev = end
+    assert levels[-1][2] == 8 and levels[-1][3] == [1, 3]
 
 
 @pytest.mark.parametrize("counts_kind", ["decode", "mixed"])
-def test_cascade_matches_oracle_and_plain_path(device, counts_kind):
+def test_cascade_matches_oracle_and_plain_path(device, counts_kind, always_cascade):
     say("cascade", counts_kind)
     cached = [2100, 2300, 300, 2100, 1700, 520, 2048, 900, 2800]
     counts = [1] * len(cached)
@@ -100,7 +110,7 @@ def test_cascade_matches_oracle_and_plain_path(device, counts_kind):
     _compare(outs[0], outs[1], "cascade vs plain")
 
 
-def test_uniform_decode_cascade_over_ticks(device):
+def test_uniform_decode_cascade_over_ticks(device, always_cascade):
     say("cascade uniform ticks")
     pool = _pool(device)
     _, caches = _shared_caches(pool, [2047, 2100, 600, 2300])
@@ -149,3 +159,59 @@ def test_attn_merge_matches_joint_softmax(device):
     torch.testing.assert_close(out_d[3:].float().cpu(), o_all, atol=2e-2, rtol=2e-2)
     torch.testing.assert_close(lse_d[:, 3:].cpu(), lse_all.t(), atol=1e-4, rtol=1e-4)
     assert not out_d[:3].float().any()
+
+
+def test_attn_merge_folds_several_parts(device):
+    say("attn merge parts")
+    g = torch.Generator(device="cpu").manual_seed(1)
+    heads, d = 4, 128
+    sizes = [29, 41, 17, 23]  # key sets of the batch-B result and three levels
+    rows = 6
+    q = torch.randn(rows, heads, d, generator=g)
+    keys = torch.randn(sum(sizes), heads, d, generator=g)
+    vals = torch.randn(sum(sizes), heads, d, generator=g)
+    edges = [0, *torch.cumsum(torch.tensor(sizes), 0).tolist()]
+
+    def part(lo, hi, r):
+        s = torch.einsum("hd,khd->hk", q[r], keys[lo:hi]) / np.sqrt(d)
+        return torch.einsum("hk,khd->hd", torch.softmax(s, dim=-1), vals[lo:hi]), torch.logsumexp(s, dim=-1)
+
+    # rows 1, 3, 4 are merged; row 1 has parts of levels 1 and 2, row 3 of levels 1-3,
+    # row 4 of level 3 only; the o_a rows are grouped by level as the cascade lays them out
+    members = {1: [1, 2], 3: [1, 2, 3], 4: [3]}
+    level_rows = {lv: [r for r in sorted(members) if lv in members[r]] for lv in (1, 2, 3)}
+    o_a, lse_a, where = [], [], {}
+    for lv in (1, 2, 3):
+        for r in level_rows[lv]:
+            o, lse = part(edges[lv], edges[lv + 1], r)
+            where[(r, lv)] = len(o_a)
+            o_a.append(o)
+            lse_a.append(lse)
+    out = torch.zeros(rows, heads, d)
+    lse_out = torch.full((heads, rows), -float("inf"))
+    want = torch.zeros(rows, heads, d)
+    for r in range(rows):
+        o, lse = part(edges[0], edges[1], r)
+        out[r], lse_out[:, r] = o, lse
+        keep = [0] + members.get(r, [])
+        idx = torch.cat([torch.arange(edges[k], edges[k + 1]) for k in keep])
+        s = torch.einsum("hd,khd->hk", q[r], keys[idx]) / np.sqrt(d)
+        want[r] = torch.einsum("hk,khd->hd", torch.softmax(s, dim=-1), vals[idx])
+    out_rows = sorted(members)
+    part_start = [0]
+    part_idx = []
+    for r in out_rows:
+        part_idx += [where[(r, lv)] for lv in members[r]]
+        part_start.append(len(part_idx))
+    out_d = out.to(torch.bfloat16).to(device)
+    lse_d = lse_out.contiguous().to(device)
+    ops.attn_merge(out_d, lse_d, torch.stack(o_a).to(torch.bfloat16).to(device),
+                   torch.stack(lse_a).t().contiguous().to(device),
+                   torch.tensor(out_rows, device=device),
+                   parts=(torch.tensor(part_start, dtype=torch.int32, device=device),
+                          torch.tensor(part_idx, dtype=torch.int32, device=device)))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out_d.float().cpu(), want, atol=2e-2, rtol=2e-2)
+    # untouched rows keep their batch-B result bit for bit
+    for r in (0, 2, 5):
+        assert torch.equal(out_d[r].cpu(), out[r].to(torch.bfloat16))
