@@ -544,13 +544,16 @@ class VarlenAttnPlan:
         scale: float | None = None,
         out: torch.Tensor | None = None,
         return_lse: bool = False,
+        lse_out: torch.Tensor | None = None,
         phases: tuple[str, ...] = ("decode", "chunk", "combine"),
         append: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
     ) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
         """Attention for one layer. ``phases`` launches a subset of the three kernels
         (decode splits, chunk rows, split combine); a full result needs all three, with
         the combine after the other two (the launch order within one call), into the
-        same ``out``. Profilers use it to time each kernel.
+        same ``out`` (and ``lse_out``, when the log-sum-exp is wanted). Profilers use it
+        to time each kernel, and ``run_overlapped`` to run decode and chunk rows on two
+        streams.
 
         ``append=(k_new, v_new, write_slots)`` first writes the tick's new K/V rows
         into the pool (index_copy_ semantics, as ``kv_append``) in the same call: decode
@@ -597,8 +600,12 @@ class VarlenAttnPlan:
             out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
         elif out.shape != query.shape or out.dtype != query.dtype or out.stride(2) != 1:
             raise ValueError("out must match the query's shape and dtype.")
-        lse = None
-        if return_lse:
+        lse = lse_out
+        if lse is not None:
+            if lse.dtype != torch.float32 or tuple(lse.shape) != (self.n_q_heads, self.total_q) \
+                    or not lse.is_contiguous():
+                raise ValueError("lse_out must be contiguous float32 [n_q_heads, total_q].")
+        elif return_lse:
             lse = torch.empty((self.n_q_heads, self.total_q), dtype=torch.float32, device=query.device)
         scale = 1.0 / math.sqrt(self.head_dim) if scale is None else float(scale)
         hints = (
@@ -638,6 +645,46 @@ class VarlenAttnPlan:
                 *hints, self.ws_ptr, self.ws_bytes, _stream_ptr(query.device))
             _capi.check(code, "hx_varlen_attn_append_run")
         return (out, lse) if return_lse else out
+
+
+def run_overlapped(plan: "VarlenAttnPlan", query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                   block_table: torch.Tensor | None, side: torch.cuda.Stream, *, return_lse: bool = False,
+                   side_first=None):
+    """``plan.run`` with the chunk rows (MFMA-bound) on ``side`` while the decode rows
+    (HBM-bound) run on the current stream; the combine runs after both. The new K/V rows
+    must already be in the pool. ``side_first`` is an optional callable queued on the
+    side stream before the chunk launch (work that must also overlap the decode rows);
+    its return value is returned last, and any tensors in it are marked as used by the
+    current stream. Falls back to ``plan.run`` when one kind of row is absent."""
+    dec, pf, _ = plan.hints
+    has_chunk = pf != 0 and plan.max_q >= 2
+    if dec == 0 or (not has_chunk and side_first is None):
+        extra = side_first() if side_first is not None else None
+        res = plan.run(query, k_cache, v_cache, block_table, return_lse=return_lse)
+        return (res, extra) if side_first is not None else res
+    main = torch.cuda.current_stream(query.device)
+    out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    lse = torch.empty((plan.n_q_heads, plan.total_q), dtype=torch.float32, device=query.device) if return_lse else None
+    forked = torch.cuda.Event()
+    forked.record(main)
+    side.wait_event(forked)
+    extra = None
+    with torch.cuda.stream(side):
+        if side_first is not None:
+            extra = side_first()
+        if has_chunk:
+            plan.run(query, k_cache, v_cache, block_table, out=out, lse_out=lse, phases=("chunk",))
+    joined = torch.cuda.Event()
+    joined.record(side)
+    plan.run(query, k_cache, v_cache, block_table, out=out, lse_out=lse, phases=("decode",))
+    main.wait_event(joined)
+    if extra is not None:
+        for t in (extra if isinstance(extra, tuple) else (extra,)):
+            if isinstance(t, torch.Tensor):
+                t.record_stream(main)
+    plan.run(query, k_cache, v_cache, block_table, out=out, lse_out=lse, phases=("combine",))
+    res = (out, lse) if return_lse else out
+    return (res, extra) if side_first is not None else res
 
 
 def varlen_attn(

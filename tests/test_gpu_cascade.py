@@ -215,3 +215,32 @@ def test_attn_merge_folds_several_parts(device):
     # untouched rows keep their batch-B result bit for bit
     for r in (0, 2, 5):
         assert torch.equal(out_d[r].cpu(), out[r].to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("cascade", [True, False])
+def test_overlapped_streams_give_the_same_bits(device, cascade, always_cascade):
+    """Chunk rows and the cascade's batch A on a second stream, decode rows on the
+    current one: the same kernels on the same inputs, so the same bits."""
+    say("overlap streams", cascade)
+    cached = [2100, 2300, 300, 2100, 1700, 520, 2048, 900, 2800]
+    counts = [1] * len(cached)
+    counts[2], counts[7] = 130, 64
+    outs = []
+    for overlap in (True, False):
+        pool = _pool(device)
+        _, caches = _shared_caches(pool, cached)
+        batch = PackedBatchCache(caches, prefix_cascade=cascade, overlap=overlap)
+        batch.prepare_packed(counts)
+        total = sum(counts)
+        g = torch.Generator(device=device).manual_seed(21)
+        for layer in range(2):
+            q = torch.randn((1, 32, total, 128), generator=g, device=device).to(torch.bfloat16)
+            k = torch.randn((1, 8, total, 128), generator=g, device=device).to(torch.bfloat16)
+            v = torch.randn((1, 8, total, 128), generator=g, device=device).to(torch.bfloat16)
+            outs.append(batch.attend(layer, q, k, v).clone())
+        torch.cuda.synchronize()
+        if overlap:
+            want = _oracle(pool, caches, counts, q[0].transpose(0, 1), layer=1)
+            _compare(outs[-1][0].transpose(0, 1).float().cpu().numpy(), want, "overlap")
+        batch.advance_packed()
+    assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])
