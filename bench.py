@@ -521,8 +521,7 @@ def full_tick_leg(device, ticks: int = 4, seed: int = 5):
                        "that prefix; 1152 packed tokens", "tokens": tokens}
     picks = {}
     for name, device_meta, fused in (("this_build", True, True), ("reference_sequence", False, False)):
-        batch = PackedBatchCache(caches, device_metadata=device_meta, prefix_cascade=device_meta,
-                                 overlap=device_meta)
+        batch = PackedBatchCache(caches, device_metadata=device_meta, prefix_cascade=device_meta)
         for _ in range(2):
             tick(batch, fused)
         torch.cuda.synchronize()
@@ -548,7 +547,7 @@ def full_tick_leg(device, ticks: int = 4, seed: int = 5):
     # How far this build's greedy picks are from the reference sequence's own maximum:
     # the two forwards round differently (attention order, fused RoPE, cascade merge), so
     # near-ties of a random-init model's flat logits may resolve differently.
-    batch = PackedBatchCache(caches, device_metadata=False, prefix_cascade=False, overlap=False)
+    batch = PackedBatchCache(caches, device_metadata=False, prefix_cascade=False)
     batch.prepare_packed(counts)
     ref_logits = model.forward_packed(input_ids, batch, fused_rope=False).float()
     for cache, n in zip(caches, lengths):
