@@ -264,6 +264,23 @@ def long_context(device, steps: int = 10, warmup: int = 3):
     assert torch.equal(kl[5][dst[3]], kl[5][src[3]]) and torch.equal(vl[35][dst[0]], vl[35][src[0]])
     del kl, vl
     torch.cuda.empty_cache()
+    # page gather (_gather_cpu's paged -> dense [1, 8, L, 128]) of one 32768-key sequence
+    pool = torch.randn((160, w.page_size, w.n_kv_heads, w.head_dim), device=device, dtype=torch.bfloat16)
+    pages = torch.randperm(160, device=device)[:128].to(torch.int32)
+    length = 128 * w.page_size
+    for _ in range(3):
+        ops.kv_gather(pool, pages, length)
+    gev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(10)]
+    for a_, b_ in gev:
+        a_.record()
+        dense = ops.kv_gather(pool, pages, length)
+        b_.record()
+    torch.cuda.synchronize()
+    gather_us = statistics.median(a_.elapsed_time(b_) for a_, b_ in gev) * 1e3
+    gather_bytes = 2 * length * w.n_kv_heads * w.head_dim * 2
+    assert torch.equal(dense[0, 3, 300], pool[int(pages[1]), 300 - 256, 3])
+    del pool, dense
+    torch.cuda.empty_cache()
     return {
         "workload": "c4: 8 decoders x 32768 keys (first 16 pages shared) + chunk 4096 rows at "
                     "positions 4096-8191; restore of 16 prefix pages x 36 layers x K/V",
@@ -275,6 +292,8 @@ def long_context(device, steps: int = 10, warmup: int = 3):
         "chunk_mfma_frac": round(w.chunk_flops() / (chunk_us * 1e-6) / 2.5e15, 4),
         "restore_copy_us": round(copy_us, 2),
         "restore_copy_gbs_rw": round(copy_bytes / (copy_us * 1e-6) / 1e9, 1),
+        "gather_32k_keys_us": round(gather_us, 2),
+        "gather_gbs_rw": round(gather_bytes / (gather_us * 1e-6) / 1e9, 1),
     }
 
 

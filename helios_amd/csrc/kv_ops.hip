@@ -144,6 +144,39 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
   }
 }
 
+// The common case: 16-byte aligned head rows, a power-of-two number of 16-byte words per
+// token row (RW = n_kv * head_b / 16) and per head row (HW), and pages holding a multiple
+// of 32 tokens. Workgroup x copies tokens [32x, 32x + 32), which share one page (one
+// page-id load); thread t moves words t + 256 i of that block, so every wave reads
+// contiguous token rows (all heads) and writes whole 256-byte head pieces. Index math
+// is shifts and masks.
+constexpr int kGatherRows = 32;
+
+template <int RW, int HW>
+__global__ __launch_bounds__(256) void kv_gather_rows_kernel(GatherArgs a) {
+  const int64_t tok0 = (int64_t)blockIdx.x * kGatherRows;
+  const int rows = (int)min((int64_t)kGatherRows, a.length - tok0);
+  const int32_t page = a.pages[tok0 / a.page_size];
+  const bool ok = page >= 0 && page < a.num_pool_pages;
+  const int64_t row0 = (int64_t)(ok ? page : 0) * a.page_size + tok0 % a.page_size;
+  const hx::u32x4_t* src = reinterpret_cast<const hx::u32x4_t*>(a.pool) + row0 * RW;
+  hx::u32x4_t* out = reinterpret_cast<hx::u32x4_t*>(a.out);
+  constexpr int kPer = kGatherRows * RW / 256;  // words per thread, all loaded before any store
+  hx::u32x4_t v[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int q = threadIdx.x + 256 * i;
+    v[i] = (ok && q / RW < rows) ? __builtin_nontemporal_load(src + q) : hx::u32x4_t{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int q = threadIdx.x + 256 * i;
+    const int jr = q / RW, wr = q & (RW - 1);
+    if (jr < rows)
+      __builtin_nontemporal_store(v[i], out + ((int64_t)(wr / HW) * a.length + tok0 + jr) * HW + (wr & (HW - 1)));
+  }
+}
+
 int grid_for(int64_t items, int threads) {
   int64_t blocks = (items + threads - 1) / threads;
   if (blocks < 1) blocks = 1;
@@ -285,8 +318,22 @@ int hx_kv_gather(const void* pool, int32_t num_pool_pages, int32_t page_size,
   a.head_b = head_dim * elem_bytes;
   const int wb = word_bytes_for({(uint64_t)a.head_b, (uint64_t)(uintptr_t)pool, (uint64_t)(uintptr_t)out});
   a.words = a.head_b / wb;
-  const int grid = grid_for((int64_t)n_kv_heads * length * a.words, 256);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (wb == 16 && page_size % kGatherRows == 0 && length / kGatherRows < 0x7fffffff) {
+    const int rw = n_kv_heads * a.head_b / 16, hw = a.head_b / 16;
+    const unsigned blocks = (unsigned)((length + kGatherRows - 1) / kGatherRows);
+    bool launched = true;
+    if (rw == 128 && hw == 16)
+      hipLaunchKernelGGL((kv_gather_rows_kernel<128, 16>), dim3(blocks), dim3(256), 0, s, a);
+    else if (rw == 64 && hw == 16)
+      hipLaunchKernelGGL((kv_gather_rows_kernel<64, 16>), dim3(blocks), dim3(256), 0, s, a);
+    else if (rw == 256 && hw == 16)
+      hipLaunchKernelGGL((kv_gather_rows_kernel<256, 16>), dim3(blocks), dim3(256), 0, s, a);
+    else
+      launched = false;
+    if (launched) return hx::status_from_hip(hipGetLastError());
+  }
+  const int grid = grid_for((int64_t)n_kv_heads * length * a.words, 256);
   switch (wb) {
     case 16: hipLaunchKernelGGL(kv_gather_kernel<uint4>, dim3(grid), dim3(256), 0, s, a); break;
     case 8: hipLaunchKernelGGL(kv_gather_kernel<uint2>, dim3(grid), dim3(256), 0, s, a); break;

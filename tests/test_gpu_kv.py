@@ -152,3 +152,15 @@ def test_gather_invalid_page_yields_zeros(device):
     got = ops.kv_gather(pool, [1, 7], 300)
     torch.cuda.synchronize()
     assert got[:, :, :256].eq(1).all() and not got[:, :, 256:].any()
+
+
+@pytest.mark.parametrize("dtype,heads,dim", [(torch.float32, 2, 6), (torch.uint8, 3, 5)])
+def test_gather_narrow_rows_take_the_generic_path(device, dtype, heads, dim):
+    """Rows that are not 16-byte multiples (24 B, 5 B) go through the element-wise kernel."""
+    say("gather generic", dtype)
+    g = torch.Generator(device="cpu").manual_seed(8)
+    pool = torch.randint(0, 255, (4, 256, heads, dim), generator=g).to(dtype).to(device)
+    got = ops.kv_gather(pool, [2, 0, 3], 700)
+    torch.cuda.synchronize()
+    ref = pool.index_select(0, torch.tensor([2, 0, 3], device=device)).reshape(-1, heads, dim)[:700]
+    assert torch.equal(got[0].permute(1, 0, 2), ref)
