@@ -126,7 +126,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_c_void_p, _i64, _i64, _c_void_p, _i64,
          _c_void_p, _i64, _i64, _c_void_p, _i64,
-         _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _c_void_p],
+         _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32, _i32, _i32, _c_void_p],
     ),
     "hx_tick_metadata": (
         ctypes.c_int,

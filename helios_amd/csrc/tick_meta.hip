@@ -171,7 +171,8 @@ __global__ __launch_bounds__(256) void merge_kernel(uint16_t* out, int64_t o_row
                                                     const uint16_t* oa, int64_t a_row, int64_t a_head,
                                                     const float* lse_a, int64_t total_a,
                                                     const int64_t* rows, const int32_t* part_start,
-                                                    const int32_t* part_idx, int64_t n_rows, int hq) {
+                                                    const int32_t* part_idx, int64_t n_parts,
+                                                    int64_t n_rows, int hq) {
   // One wave per (entry j, head h); lane l owns dims l and l + 64. Every lane reads the old
   // lse before lane 0 stores the merged one, in program order within the wave.
   const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -182,9 +183,9 @@ __global__ __launch_bounds__(256) void merge_kernel(uint16_t* out, int64_t o_row
   const int64_t r = rows[j];
   if (r < 0 || r >= total_out) return;
   int64_t p0 = j, p1 = j + 1;
-  if (part_start != nullptr) {
-    p0 = part_start[j];
-    p1 = part_start[j + 1];
+  if (part_start != nullptr) {  // a range outside the part list is clipped to it
+    p0 = max((int64_t)part_start[j], (int64_t)0);
+    p1 = min((int64_t)part_start[j + 1], n_parts);
   }
   float* lb_p = lse_out + (int64_t)h * total_out + r;
   float m = *lb_p;  // the running result is normalised, with log-sum-exp m
@@ -222,12 +223,12 @@ extern "C" int hx_attn_merge(void* out, int64_t out_row_stride, int64_t out_head
                              const void* o_a, int64_t a_row_stride, int64_t a_head_stride,
                              const float* lse_a, int64_t total_a,
                              const int64_t* rows, const int32_t* part_start, const int32_t* part_idx,
-                             int64_t n_rows, int32_t n_heads, int32_t head_dim, int32_t dtype,
-                             void* stream) {
+                             int64_t n_parts, int64_t n_rows, int32_t n_heads, int32_t head_dim,
+                             int32_t dtype, void* stream) {
   if (head_dim != 128 || (dtype != HX_DTYPE_BF16 && dtype != HX_DTYPE_FP16)) return HX_E_UNSUPPORTED;
   if (n_rows < 0 || n_heads < 1 || total_out < 0 || total_a < 0) return HX_E_INVALID_ARG;
   if (part_start == nullptr && total_a < n_rows) return HX_E_INVALID_ARG;
-  if ((part_start == nullptr) != (part_idx == nullptr)) return HX_E_INVALID_ARG;
+  if ((part_start == nullptr) != (part_idx == nullptr) || n_parts < 0) return HX_E_INVALID_ARG;
   if (n_rows == 0) return HX_OK;
   if (!out || !lse_out || !o_a || !lse_a || !rows) return HX_E_INVALID_ARG;
   const int64_t items = n_rows * n_heads;
@@ -239,10 +240,10 @@ extern "C" int hx_attn_merge(void* out, int64_t out_row_stride, int64_t out_head
   if (dtype == HX_DTYPE_BF16)
     hipLaunchKernelGGL(merge_kernel<__bf16>, dim3(grid), dim3(256), 0, s, o, out_row_stride, out_head_stride,
                        lse_out, total_out, a, a_row_stride, a_head_stride, lse_a, total_a, rows, part_start,
-                       part_idx, n_rows, n_heads);
+                       part_idx, n_parts, n_rows, n_heads);
   else
     hipLaunchKernelGGL(merge_kernel<_Float16>, dim3(grid), dim3(256), 0, s, o, out_row_stride, out_head_stride,
                        lse_out, total_out, a, a_row_stride, a_head_stride, lse_a, total_a, rows, part_start,
-                       part_idx, n_rows, n_heads);
+                       part_idx, n_parts, n_rows, n_heads);
   return hx::status_from_hip(hipGetLastError());
 }

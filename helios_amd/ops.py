@@ -201,6 +201,7 @@ def attn_merge(out: torch.Tensor, lse_out: torch.Tensor, o_a: torch.Tensor, lse_
     if rows.dtype != torch.int64 or rows.ndim != 1 or not rows.is_contiguous():
         raise ValueError("rows must be contiguous int64 [n].")
     start_ptr = idx_ptr = None
+    n_parts = 0
     if parts is None:
         if n != n_a:
             raise ValueError("without parts, rows must have one entry per o_a row.")
@@ -212,13 +213,14 @@ def attn_merge(out: torch.Tensor, lse_out: torch.Tensor, o_a: torch.Tensor, lse_
         if part_start.numel() != n + 1:
             raise ValueError("part_start must have one entry per row plus one.")
         start_ptr, idx_ptr = part_start.data_ptr(), part_idx.data_ptr()
+        n_parts = part_idx.numel()
     dtype = _SUPPORTED.get(out.dtype)
     if dtype is None:
         raise ValueError("attention outputs must be bfloat16 or float16.")
     code = _capi.lib().hx_attn_merge(
         out.data_ptr(), out.stride(0), out.stride(1), lse_out.data_ptr(), out.shape[0],
         o_a.data_ptr(), o_a.stride(0), o_a.stride(1), lse_a.data_ptr(), lse_a.stride(0) if heads > 1 else n_a,
-        rows.data_ptr(), start_ptr, idx_ptr, n, heads, o_a.shape[2], dtype, _stream_ptr(device),
+        rows.data_ptr(), start_ptr, idx_ptr, n_parts, n, heads, o_a.shape[2], dtype, _stream_ptr(device),
     )
     _capi.check(code, "hx_attn_merge")
 

@@ -283,8 +283,9 @@ int hx_qk_norm_rope_append(const void* q, int64_t q_row_stride, int64_t q_head_s
  * shared-prefix split of PagedBatchCache.attend; no counterpart in the reference, whose
  * varlen_attn reads every sequence's prefix pages itself). Entry j < n_rows merges its
  * parts into packed row r = rows[j] of (out, lse_out), in place: the parts are rows
- * part_idx[part_start[j]] .. part_idx[part_start[j + 1] - 1] of (o_a, lse_a), or o_a
- * row j alone when part_start and part_idx are NULL. For head h, folding one part a
+ * part_idx[part_start[j]] .. part_idx[part_start[j + 1] - 1] of (o_a, lse_a), the range
+ * clipped to [0, n_parts), or o_a row j alone when part_start and part_idx are NULL
+ * (n_parts is then ignored). For head h, folding one part a
  * into the running result b (initially out[r][h], lse_out[h][r]) with m = max(lse_a, lse_b):
  *   o   = (o_a e^(lse_a - m) + o_b e^(lse_b - m)) / (e^(lse_a - m) + e^(lse_b - m))
  *   lse = m + log(e^(lse_a - m) + e^(lse_b - m))
@@ -299,7 +300,8 @@ int hx_attn_merge(void* out, int64_t out_row_stride, int64_t out_head_stride,
                   const void* o_a, int64_t a_row_stride, int64_t a_head_stride,
                   const float* lse_a, int64_t total_a,
                   const int64_t* rows, const int32_t* part_start, const int32_t* part_idx,
-                  int64_t n_rows, int32_t n_heads, int32_t head_dim, int32_t dtype, void* stream);
+                  int64_t n_parts, int64_t n_rows, int32_t n_heads, int32_t head_dim,
+                  int32_t dtype, void* stream);
 
 int hx_tick_metadata(const int32_t* seq, int32_t batch, int32_t total_q, int32_t n_logits,
                      const int32_t* block_table, int32_t block_table_stride,
