@@ -8,8 +8,9 @@
 // keys are normalised, rotated and stored straight into their pool rows, and values are
 // copied into theirs; the rotated keys never make a round trip through HBM.
 //
-// One workgroup per packed row, one wave per head at a time; lane l owns dims l and
-// l + 64, which are exactly the pair that RoPE mixes. The arithmetic follows the reference's op order with no fused
+// One workgroup per packed row. The 16-byte-access kernel (aligned rows) gives each head
+// 16 lanes of 8 dims; the 2-byte-access kernel gives each head a wave, lane l owning dims
+// l and l + 64, which are exactly the pair that RoPE mixes. The arithmetic follows the reference's op order with no fused
 // multiply-adds: n = bf16((x * rsqrt(mean(x^2) + eps)) * w), then
 // out = bf16(n * cos + (-n') * sin).
 
@@ -97,6 +98,90 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_append_kernel(RopeA
   }
 }
 
+// The same computation with 16-byte accesses, for 16-byte aligned rows (the common case):
+// a head row is 16 lanes x 8 dims, so each wave takes four heads at a time. Lane j of a
+// head owns dims 8j .. 8j + 7; the RoPE partner of dim d (d +- 64) sits in lane j ^ 8 at
+// the same position and comes over in four packed 32-bit shuffles. The sum of squares is
+// reduced over the 16 lanes of the head; the element arithmetic is the scalar kernel's.
+template <typename T>
+__global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_append_vec_kernel(RopeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sub = lane >> 4, j = lane & 15;
+  const int64_t row = blockIdx.x;
+  const int heads = a.hq + 2 * a.hkv;
+  const int64_t slot = a.slots[row];
+  const bool slot_ok = slot >= 0 && slot < a.pool_rows;
+  int64_t pos = a.positions[row];
+  pos = pos < 0 ? 0 : (pos >= a.rope_rows ? a.rope_rows - 1 : pos);
+  float c[8], sn[8], wq[8], wk[8];
+  {
+    const float4* cp = reinterpret_cast<const float4*>(a.cos + pos * kRopeD + 8 * j);
+    const float4* sp = reinterpret_cast<const float4*>(a.sin + pos * kRopeD + 8 * j);
+    const float4* qp = reinterpret_cast<const float4*>(a.q_scale + 8 * j);
+    const float4* kp = reinterpret_cast<const float4*>(a.k_scale + 8 * j);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float4 c4 = cp[h], s4 = sp[h], q4 = qp[h], k4 = kp[h];
+      c[4 * h] = c4.x; c[4 * h + 1] = c4.y; c[4 * h + 2] = c4.z; c[4 * h + 3] = c4.w;
+      sn[4 * h] = s4.x; sn[4 * h + 1] = s4.y; sn[4 * h + 2] = s4.z; sn[4 * h + 3] = s4.w;
+      wq[4 * h] = q4.x; wq[4 * h + 1] = q4.y; wq[4 * h + 2] = q4.z; wq[4 * h + 3] = q4.w;
+      wk[4 * h] = k4.x; wk[4 * h + 1] = k4.y; wk[4 * h + 2] = k4.z; wk[4 * h + 3] = k4.w;
+    }
+  }
+  for (int h0 = 4 * wave; h0 < heads; h0 += kRopeThreads / 16) {
+    const int h = h0 + sub;
+    if (h >= heads) continue;  // whole 16-lane groups drop out together
+    if (h >= a.hq + a.hkv) {   // value head: plain copy into the pool
+      if (!slot_ok) continue;
+      const int hv = h - a.hq - a.hkv;
+      const uint4 val = *reinterpret_cast<const uint4*>(a.v + row * a.v_row + hv * a.v_head + 8 * j);
+      *reinterpret_cast<uint4*>(a.v_pool + (slot * a.hkv + hv) * kRopeD + 8 * j) = val;
+      continue;
+    }
+    const bool is_q = h < a.hq;
+    const int hh = is_q ? h : h - a.hq;
+    if (!is_q && !slot_ok) continue;
+    const uint4 raw = *reinterpret_cast<const uint4*>(
+        is_q ? a.q + row * a.q_row + hh * a.q_head + 8 * j : a.k + row * a.k_row + hh * a.k_head + 8 * j);
+    const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+    float x[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      x[2 * q] = hx::Elem<T>::lo(rw[q]);
+      x[2 * q + 1] = hx::Elem<T>::hi(rw[q]);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = __fadd_rn(ss, __fmul_rn(x[e], x[e]));
+#pragma unroll
+    for (int m = 1; m <= 8; m <<= 1) ss = __fadd_rn(ss, __shfl_xor(ss, m));
+    const float r = rsqrtf(__fadd_rn(__fdiv_rn(ss, (float)kRopeD), a.eps));
+    uint32_t np[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      np[q] = hx::pack2_round<T>(__fmul_rn(__fmul_rn(x[2 * q], r), is_q ? wq[2 * q] : wk[2 * q]),
+                                 __fmul_rn(__fmul_rn(x[2 * q + 1], r), is_q ? wq[2 * q + 1] : wk[2 * q + 1]));
+    const bool low = j < 8;  // dims < 64: out = n c - n' s; else out = n c + n' s
+    uint32_t op[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t pp = (uint32_t)__shfl_xor((int)np[q], 8);
+      float o[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float n = e ? hx::Elem<T>::hi(np[q]) : hx::Elem<T>::lo(np[q]);
+        const float np_ = e ? hx::Elem<T>::hi(pp) : hx::Elem<T>::lo(pp);
+        o[e] = __fadd_rn(__fmul_rn(n, c[2 * q + e]), __fmul_rn(low ? -np_ : np_, sn[2 * q + e]));
+      }
+      op[q] = hx::pack2_round<T>(o[0], o[1]);
+    }
+    uint16_t* dst = is_q ? a.q_out + row * a.qo_row + hh * a.qo_head + 8 * j
+                         : a.k_pool + (slot * a.hkv + hh) * kRopeD + 8 * j;
+    *reinterpret_cast<uint4*>(dst) = make_uint4(op[0], op[1], op[2], op[3]);
+  }
+}
+
 }  // namespace
 
 extern "C" int hx_qk_norm_rope_append(
@@ -146,9 +231,21 @@ extern "C" int hx_qk_norm_rope_append(
   if (n_rows > 0x7fffffff) return HX_E_INVALID_ARG;
   const unsigned grid = (unsigned)n_rows;  // one workgroup per packed row
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (dtype == HX_DTYPE_BF16)
-    hipLaunchKernelGGL(qk_norm_rope_append_kernel<__bf16>, dim3(grid), dim3(kRopeThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(qk_norm_rope_append_kernel<_Float16>, dim3(grid), dim3(kRopeThreads), 0, s, a);
+  // 16-byte path when every row, head and table start is 16-byte aligned.
+  const uintptr_t ptrs = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                         reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(q_out) |
+                         reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool) |
+                         reinterpret_cast<uintptr_t>(cos) | reinterpret_cast<uintptr_t>(sin) |
+                         reinterpret_cast<uintptr_t>(q_norm_weight) | reinterpret_cast<uintptr_t>(k_norm_weight);
+  const int64_t strides = q_row_stride | q_head_stride | k_row_stride | k_head_stride | v_row_stride |
+                          v_head_stride | q_out_row_stride | q_out_head_stride;
+  const bool vec = (ptrs & 15) == 0 && (strides & 7) == 0;
+  if (dtype == HX_DTYPE_BF16) {
+    if (vec) hipLaunchKernelGGL(qk_norm_rope_append_vec_kernel<__bf16>, dim3(grid), dim3(kRopeThreads), 0, s, a);
+    else hipLaunchKernelGGL(qk_norm_rope_append_kernel<__bf16>, dim3(grid), dim3(kRopeThreads), 0, s, a);
+  } else {
+    if (vec) hipLaunchKernelGGL(qk_norm_rope_append_vec_kernel<_Float16>, dim3(grid), dim3(kRopeThreads), 0, s, a);
+    else hipLaunchKernelGGL(qk_norm_rope_append_kernel<_Float16>, dim3(grid), dim3(kRopeThreads), 0, s, a);
+  }
   return hx::status_from_hip(hipGetLastError());
 }

@@ -32,11 +32,14 @@ def pair_close(got: torch.Tensor, ref: torch.Tensor) -> bool:
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rows", [1, 7, 300])
-def test_kernel_matches_oracle_and_reference_ops(device, dtype, rows):
-    say("qk rope", dtype, rows)
+@pytest.mark.parametrize("offset", [0, 1], ids=["aligned16", "unaligned"])
+def test_kernel_matches_oracle_and_reference_ops(device, dtype, rows, offset):
+    """offset 0: 16-byte aligned rows (the 16-byte-access kernel); offset 1 shifts the
+    projection by one element, which sends the launch to the 2-byte-access kernel."""
+    say("qk rope", dtype, rows, offset)
     g = torch.Generator(device="cpu").manual_seed(rows)
     hq, hkv, d = 32, 8, 128
-    proj = torch.randn(rows, (hq + 2 * hkv) * d, generator=g).to(dtype).to(device)
+    proj = torch.randn(rows, (hq + 2 * hkv) * d + offset, generator=g).to(dtype).to(device)[:, offset:]
     q = proj[:, : hq * d].view(rows, hq, d)              # strided views of one projection
     k = proj[:, hq * d:(hq + hkv) * d].view(rows, hkv, d)
     v = proj[:, (hq + hkv) * d:].view(rows, hkv, d)
