@@ -37,6 +37,7 @@ namespace {
 constexpr int kD = 128;          // head_dim built
 constexpr int kSplit = 256;      // keys per decode workgroup
 constexpr int kThreads = 256;    // 4 wavefronts
+constexpr int kXcds = 8;         // XCDs of an MI355X (gfx950); workgroups are dealt round-robin
 constexpr int kTile = 64;        // keys per chunk-kernel tile
 constexpr int kPlanThreads = 1024;
 // Chunk split-K: when the chunk work items would launch fewer than kChunkFillWGs
@@ -515,8 +516,14 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, held in a scalar register
-  const int item = (int)blockIdx.x / a.hkv;
-  const int g = (int)blockIdx.x - item * a.hkv;
+  // XCD-aware order: workgroups go to the kXcds XCDs round-robin, so the hkv consecutive
+  // workgroups an XCD receives are the KV heads of one split; each XCD then streams whole
+  // token rows of the pages it reads (about 4 % faster than one head per XCD). The grid
+  // covers the work items rounded up to a multiple of kXcds.
+  const int xcd = (int)blockIdx.x % kXcds, jx = (int)blockIdx.x / kXcds;
+  const int g = jx % a.hkv;
+  const int item = (jx / a.hkv) * kXcds + xcd;
+  if (item >= a.grid_dec) return;
   // The work item is read together with the header (item < grid_dec <= the list's
   // capacity, so the read stays inside the workspace) and used only once both check out.
   const Header hd = read_header(a);
@@ -1143,11 +1150,14 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
 // ------------------------------------------------------------------ host helpers
 bool valid_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
 
+// Decode work items the launch covers: grid_dec rounded up to whole rounds of the XCDs.
+int64_t decode_grid(int64_t grid_dec) { return (grid_dec + kXcds - 1) / kXcds * kXcds; }
+
 template <typename T, int G>
 int launch_run(const RunArgs& a, hipStream_t s) {
   // The combine merges decode and chunk split partials, so it runs last.
   if (a.grid_dec > 0)
-    hipLaunchKernelGGL((decode_kernel<T, G>), dim3((unsigned)(a.grid_dec * a.hkv)), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((decode_kernel<T, G>), dim3((unsigned)(decode_grid(a.grid_dec) * a.hkv)), dim3(kThreads), 0, s, a);
   if (a.grid_pf > 0)
     hipLaunchKernelGGL((chunk_kernel<T, G>), dim3((unsigned)(a.grid_pf * a.hkv)), dim3(kChunkThreads), 0, s, a);
   if (a.grid_comb > 0)
@@ -1372,7 +1382,7 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
   a.grid_dec = clamp_hint(decode_items_hint, l.max_dec);
   a.grid_pf = max_q >= 2 ? clamp_hint(prefill_items_hint, l.max_pf) : 0;
   a.grid_comb = clamp_hint(combine_seqs_hint, l.max_comb);
-  if ((int64_t)a.grid_dec * n_kv_heads > INT32_MAX || (int64_t)a.grid_pf * n_kv_heads > INT32_MAX)
+  if (decode_grid(a.grid_dec) * n_kv_heads > INT32_MAX || (int64_t)a.grid_pf * n_kv_heads > INT32_MAX)
     return HX_E_INVALID_ARG;
   a.k_new = nullptr;
   a.v_new = nullptr;
