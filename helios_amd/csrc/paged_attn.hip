@@ -735,14 +735,100 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
 // ------------------------------------------------------------------ split combine
 // A combine record {b, first slot, splits | (rows - 1) << 24, first output row} covers
 // `rows` consecutive output rows (1 for a decode row, up to kCombRows rows of a split
-// chunk block) whose partials sit at slots first + r * splits + s. One thread per (row,
+// chunk block) whose partials sit at slots first + r * splits + s. A task is one (row,
 // head, 8-dim chunk): 16-byte partial loads, merged with an online max in groups of
-// kCombChunk splits whose (m, l) pairs and partial rows are loaded together.
+// kCombChunk splits whose (m, l) pairs and partial rows are loaded together. When the
+// record has fewer tasks than threads, the workgroup splits the partials into
+// kCombThreads / tasks contiguous ranges (a decode row at G = 4: eight, two per wave),
+// and the ranges are merged in LDS in range order, so the result does not depend on
+// scheduling.
 constexpr int kCombChunk = 8;
+constexpr int kCombThreads = 512;
+
+struct CombAcc {
+  float m, l;
+  float acc[8];
+};
+
+// Merges the partials of splits [s0, s_end), s_end - s0 <= NC, into r: the NC (m, l)
+// pairs and partial rows are loaded together (indices past s_end re-read s_end - 1 and
+// get weight 0).
+template <int NC>
+__device__ __forceinline__ void combine_step(const float2* ml, const uint16_t* po, int64_t step_ml,
+                                             int64_t step_o, int s0, int s_end, CombAcc& r) {
+  float2 mlv[NC];
+  uint4 ov[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int sj = s0 + j < s_end ? s0 + j : s_end - 1;
+    mlv[j] = ml[(int64_t)sj * step_ml];
+    ov[j] = *reinterpret_cast<const uint4*>(po + (int64_t)sj * step_o);
+  }
+  float cm = r.m;
+#pragma unroll
+  for (int j = 0; j < NC; ++j)
+    if (s0 + j < s_end) cm = fmaxf(cm, mlv[j].x);
+  if (cm == -INFINITY) return;
+  const float rescale = r.m == -INFINITY ? 0.f : hx::fast_exp2(r.m - cm);
+  r.l *= rescale;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r.acc[e] *= rescale;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const bool live = s0 + j < s_end && mlv[j].x != -INFINITY;
+    const float wgt = live ? hx::fast_exp2(mlv[j].x - cm) * mlv[j].y : 0.f;  // partial stores o / l
+    r.l += wgt;
+    const uint32_t w4[4] = {ov[j].x, ov[j].y, ov[j].z, ov[j].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      r.acc[2 * e] += wgt * hx::Elem<__bf16>::lo(w4[e]);
+      r.acc[2 * e + 1] += wgt * hx::Elem<__bf16>::hi(w4[e]);
+    }
+  }
+  r.m = cm;
+}
+
+// Online merge of the partials of splits [s_lo, s_hi) for one task, in split order:
+// (m, l, acc) with acc = sum over splits of 2^(m_s - m) * l_s * (o_s / l_s), so the
+// output is acc / l. Groups of kCombChunk while more than two splits remain, then a
+// tail of at most two (records of one or two splits load only those).
+__device__ __forceinline__ CombAcc combine_range(const RunArgs& a, int64_t base, int qh, int ch,
+                                                 int s_lo, int s_hi) {
+  const float2* ml = a.part_ml + base * a.hq + qh;
+  const uint16_t* po = a.part_o + (base * a.hq + qh) * kD + 8 * ch;
+  const int64_t step_o = (int64_t)a.hq * kD;
+  CombAcc r;
+  r.m = -INFINITY;
+  r.l = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r.acc[e] = 0.f;
+  int s0 = s_lo;
+  for (; s_hi - s0 > 2; s0 += kCombChunk) combine_step<kCombChunk>(ml, po, a.hq, step_o, s0, min(s_hi, s0 + kCombChunk), r);
+  if (s_hi > s0) combine_step<2>(ml, po, a.hq, step_o, s0, s_hi, r);
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ void combine_store(const RunArgs& a, const CombAcc& r, int row, int qh, int ch) {
+  const float inv = r.l > 0.f ? 1.f / r.l : 0.f;
+  const uint4 u = make_uint4(hx::pack2_round<T>(r.acc[0] * inv, r.acc[1] * inv), hx::pack2_round<T>(r.acc[2] * inv, r.acc[3] * inv),
+                             hx::pack2_round<T>(r.acc[4] * inv, r.acc[5] * inv), hx::pack2_round<T>(r.acc[6] * inv, r.acc[7] * inv));
+  T* orow = reinterpret_cast<T*>(a.out) + (int64_t)row * a.o_row + (int64_t)qh * a.o_head + 8 * ch;
+  if (a.o_row % 8 == 0 && a.o_head % 8 == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0) {
+    *reinterpret_cast<uint4*>(orow) = u;
+  } else {
+    uint2* o2 = reinterpret_cast<uint2*>(orow);  // rows are 8-byte aligned (checked on the host)
+    o2[0] = make_uint2(u.x, u.y);
+    o2[1] = make_uint2(u.z, u.w);
+  }
+  if (a.lse && ch == 0)
+    a.lse[(int64_t)qh * a.total_q + row] = r.l > 0.f ? (r.m + log2f(r.l)) * kLn2 : -INFINITY;
+}
 
 template <typename T, int G>
-__global__ __launch_bounds__(kThreads) void combine_kernel(RunArgs a) {
-  constexpr int kPerRow = G * (kD / 8);  // threads per output row
+__global__ __launch_bounds__(kCombThreads, 4) void combine_kernel(RunArgs a) {
+  constexpr int kPerRow = G * (kD / 8);  // tasks per output row
+  __shared__ float sh[10][kCombThreads];     // (m, l, acc[8]) of every range, one column per thread
   const int cs = (int)blockIdx.x / a.hkv;
   const int g = (int)blockIdx.x - cs * a.hkv;
   const Header hd = read_header(a);
@@ -755,63 +841,51 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(RunArgs a) {
   if ((unsigned)c.x >= (unsigned)a.batch || first < 0 || splits < 1 || rows > kCombRows) return;
   if ((int64_t)first + (int64_t)rows * splits > a.slot_cap) return;
   if (q0 < 0 || q0 + rows > a.total_q) return;
-  for (int t = threadIdx.x; t < rows * kPerRow; t += kThreads) {
-    const int r = t / kPerRow;
-    const int h = (t - r * kPerRow) >> 4, ch = t & 15;
-    const int qh = g * G + h;
-    const int64_t base = (int64_t)first + (int64_t)r * splits;
-    const float2* ml = a.part_ml + base * a.hq + qh;
-    const uint16_t* po = a.part_o + (base * a.hq + qh) * kD + 8 * ch;
-    const int64_t step_o = (int64_t)a.hq * kD;
-    float m_run = -INFINITY, l_run = 0.f;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < splits; s0 += kCombChunk) {
-      float2 mlv[kCombChunk];
-      uint4 ov[kCombChunk];
+  const int tasks = rows * kPerRow;
+  const int ranges = min(kCombThreads / tasks, splits);  // workgroup-uniform
+  if (ranges <= 1) {
+    for (int t = threadIdx.x; t < tasks; t += kCombThreads) {
+      const int r = t / kPerRow;
+      const int h = (t - r * kPerRow) >> 4, ch = t & 15;
+      const CombAcc res = combine_range(a, (int64_t)first + (int64_t)r * splits, g * G + h, ch, 0, splits);
+      combine_store<T>(a, res, q0 + r, g * G + h, ch);
+    }
+    return;
+  }
+  // ranges >= 2: thread t < ranges * tasks takes task t % tasks over range t / tasks.
+  const int t = threadIdx.x;
+  const int task = t % tasks, rg = t / tasks;
+  const int r = task / kPerRow;
+  const int h = (task - r * kPerRow) >> 4, ch = task & 15;
+  const int span = (splits + ranges - 1) / ranges;
+  if (rg < ranges) {
+    const int s_lo = min(splits, rg * span), s_hi = min(splits, s_lo + span);
+    const CombAcc res = combine_range(a, (int64_t)first + (int64_t)r * splits, g * G + h, ch, s_lo, s_hi);
+    sh[0][t] = res.m;
+    sh[1][t] = res.l;
 #pragma unroll
-      for (int j = 0; j < kCombChunk; ++j) {
-        const int sj = s0 + j < splits ? s0 + j : splits - 1;  // clamp: duplicates get weight 0
-        mlv[j] = ml[(int64_t)sj * a.hq];
-        ov[j] = *reinterpret_cast<const uint4*>(po + (int64_t)sj * step_o);
-      }
-      float cm = m_run;
+    for (int e = 0; e < 8; ++e) sh[2 + e][t] = res.acc[e];
+  }
+  __syncthreads();
+  if (rg == 0) {
+    float m = -INFINITY;
+    for (int q = 0; q < ranges; ++q) m = fmaxf(m, sh[0][q * tasks + task]);
+    CombAcc res;
+    res.m = m;
+    res.l = 0.f;
 #pragma unroll
-      for (int j = 0; j < kCombChunk; ++j)
-        if (s0 + j < splits) cm = fmaxf(cm, mlv[j].x);
-      if (cm != -INFINITY) {
-        const float rescale = m_run == -INFINITY ? 0.f : hx::fast_exp2(m_run - cm);
-        l_run *= rescale;
+    for (int e = 0; e < 8; ++e) res.acc[e] = 0.f;
+    if (m != -INFINITY) {
+      for (int q = 0; q < ranges; ++q) {
+        const int col = q * tasks + task;
+        const float mq = sh[0][col];
+        const float wq = mq == -INFINITY ? 0.f : hx::fast_exp2(mq - m);
+        res.l += wq * sh[1][col];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] *= rescale;
-#pragma unroll
-        for (int j = 0; j < kCombChunk; ++j) {
-          const bool live = s0 + j < splits && mlv[j].x != -INFINITY;
-          const float wgt = live ? hx::fast_exp2(mlv[j].x - cm) * mlv[j].y : 0.f;  // partial stores o / l
-          l_run += wgt;
-          const uint32_t w4[4] = {ov[j].x, ov[j].y, ov[j].z, ov[j].w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            acc[2 * e] += wgt * hx::Elem<__bf16>::lo(w4[e]);
-            acc[2 * e + 1] += wgt * hx::Elem<__bf16>::hi(w4[e]);
-          }
-        }
-        m_run = cm;
+        for (int e = 0; e < 8; ++e) res.acc[e] += wq * sh[2 + e][col];
       }
     }
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-    const int row = q0 + r;
-    const uint4 u = make_uint4(hx::pack2_round<T>(acc[0] * inv, acc[1] * inv), hx::pack2_round<T>(acc[2] * inv, acc[3] * inv),
-                               hx::pack2_round<T>(acc[4] * inv, acc[5] * inv), hx::pack2_round<T>(acc[6] * inv, acc[7] * inv));
-    T* orow = reinterpret_cast<T*>(a.out) + (int64_t)row * a.o_row + (int64_t)qh * a.o_head + 8 * ch;
-    if (a.o_row % 8 == 0 && a.o_head % 8 == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0) {
-      *reinterpret_cast<uint4*>(orow) = u;
-    } else {
-      uint2* o2 = reinterpret_cast<uint2*>(orow);  // rows are 8-byte aligned (checked on the host)
-      o2[0] = make_uint2(u.x, u.y);
-      o2[1] = make_uint2(u.z, u.w);
-    }
-    if (a.lse && ch == 0)
-      a.lse[(int64_t)qh * a.total_q + row] = l_run > 0.f ? (m_run + log2f(l_run)) * kLn2 : -INFINITY;
+    combine_store<T>(a, res, q0 + r, g * G + h, ch);
   }
 }
 
@@ -1161,7 +1235,7 @@ int launch_run(const RunArgs& a, hipStream_t s) {
   if (a.grid_pf > 0)
     hipLaunchKernelGGL((chunk_kernel<T, G>), dim3((unsigned)(a.grid_pf * a.hkv)), dim3(kChunkThreads), 0, s, a);
   if (a.grid_comb > 0)
-    hipLaunchKernelGGL((combine_kernel<T, G>), dim3((unsigned)(a.grid_comb * a.hkv)), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((combine_kernel<T, G>), dim3((unsigned)(a.grid_comb * a.hkv)), dim3(kCombThreads), 0, s, a);
   return hx::status_from_hip(hipGetLastError());
 }
 
