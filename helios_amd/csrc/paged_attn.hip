@@ -790,8 +790,9 @@ __device__ __forceinline__ void combine_step(const float2* ml, const uint16_t* p
 
 // Online merge of the partials of splits [s_lo, s_hi) for one task, in split order:
 // (m, l, acc) with acc = sum over splits of 2^(m_s - m) * l_s * (o_s / l_s), so the
-// output is acc / l. Groups of kCombChunk while more than two splits remain, then a
-// tail of at most two (records of one or two splits load only those).
+// output is acc / l. Groups of kCombChunk while more than four splits remain (the last
+// of them may re-read clamped entries), then one group of four or two: records of up to
+// four splits load no more than the next power of two.
 __device__ __forceinline__ CombAcc combine_range(const RunArgs& a, int64_t base, int qh, int ch,
                                                  int s_lo, int s_hi) {
   const float2* ml = a.part_ml + base * a.hq + qh;
@@ -803,8 +804,11 @@ __device__ __forceinline__ CombAcc combine_range(const RunArgs& a, int64_t base,
 #pragma unroll
   for (int e = 0; e < 8; ++e) r.acc[e] = 0.f;
   int s0 = s_lo;
-  for (; s_hi - s0 > 2; s0 += kCombChunk) combine_step<kCombChunk>(ml, po, a.hq, step_o, s0, min(s_hi, s0 + kCombChunk), r);
-  if (s_hi > s0) combine_step<2>(ml, po, a.hq, step_o, s0, s_hi, r);
+  for (; s_hi - s0 > 4; s0 += kCombChunk) combine_step<kCombChunk>(ml, po, a.hq, step_o, s0, min(s_hi, s0 + kCombChunk), r);
+  if (s_hi - s0 > 2)
+    combine_step<4>(ml, po, a.hq, step_o, s0, s_hi, r);
+  else if (s_hi > s0)
+    combine_step<2>(ml, po, a.hq, step_o, s0, s_hi, r);
   return r;
 }
 
