@@ -67,6 +67,21 @@ def test_windows(device, window):
     compare(tick.attend(window=window, exact_grid=True), ref, what=f"window {window}")
 
 
+@pytest.mark.parametrize("page_size", [512, 768])
+def test_page_sizes_beyond_256(device, page_size):
+    """Pages of any multiple of 256 tokens: decode splits and chunk tiles index a page
+    as (page id, offset), so a split or tile may start mid-page."""
+    say("page size", page_size)
+    w = synth.small_mixed(40 + page_size // 256, batch=6, max_cached=1800, max_chunk=300,
+                          num_pages=48, page_size=page_size)
+    tick = DeviceTick(w, torch.bfloat16, device)
+    ref, ref_lse = tick.oracle()
+    out, lse = tick.attend(exact_grid=True, return_lse=True)
+    compare(out, ref, what=f"page size {page_size}")
+    assert np.abs(lse.cpu().numpy() - ref_lse).max() < 5e-3
+    assert torch.equal(tick.attend().view(torch.int16), out.view(torch.int16))
+
+
 def test_c2_decode_tick(device):
     say("c2 decode tick")
     w = synth.c2()
