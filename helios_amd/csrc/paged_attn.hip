@@ -489,16 +489,14 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, hx::dpp<hx::kDppXor2>(v));
   v = fmaxf(v, hx::dpp<hx::kDppHalfMirror>(v));
   v = fmaxf(v, hx::dpp<hx::kDppMirror>(v));
-  v = fmaxf(v, __shfl_xor(v, 16));
-  return fmaxf(v, __shfl_xor(v, 32));
+  return hx::max_xor32(hx::max_xor16(v));
 }
 __device__ __forceinline__ float wave_sum(float v) {
   v += hx::dpp<hx::kDppXor1>(v);
   v += hx::dpp<hx::kDppXor2>(v);
   v += hx::dpp<hx::kDppHalfMirror>(v);
   v += hx::dpp<hx::kDppMirror>(v);
-  v += __shfl_xor(v, 16);
-  return v + __shfl_xor(v, 32);
+  return hx::add_xor32(hx::add_xor16(v));
 }
 
 template <typename T, int G>
@@ -1127,8 +1125,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
 #pragma unroll
       for (int kb = 1; kb < 4; ++kb)
         mx = fmaxf(mx, fmaxf(fmaxf(sacc[kb][rb][0], sacc[kb][rb][1]), fmaxf(sacc[kb][rb][2], sacc[kb][rb][3])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = hx::max_xor32(hx::max_xor16(mx));
       // Lazy max: the row's reference max moves only when the tile max exceeds it by more
       // than kLazyLog2 (log2 units). Until then p = 2^((s - m_run) * sl2) <= 2^kLazyLog2,
       // which the fp32 sums and bf16 P carry as accurately as p <= 1. With m_run = -inf
@@ -1189,9 +1186,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   const int64_t slot0 = S > 1 ? a.dec_cap + a.pf_base[item] + sp : 0;
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
-    float l = l_run[rb];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    const float l = hx::add_xor32(hx::add_xor16(l_run[rb]));
     const int rr = wr0 + 16 * rb + (lane & 15);
     if (rr < n && S > 1) {
       const int64_t slot = slot0 + (int64_t)(rr - row0) * S;
