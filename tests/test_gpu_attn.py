@@ -82,6 +82,22 @@ def test_page_sizes_beyond_256(device, page_size):
     assert torch.equal(tick.attend().view(torch.int16), out.view(torch.int16))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_large_logits_sharp_softmax(device, dtype):
+    """Queries scaled by 40: scores reach thousands and each row's softmax is close to
+    one-hot, so the running max moves by large steps between tiles and splits (the
+    rescale and combine paths) and no exponent may overflow."""
+    say("large logits", dtype)
+    w = synth.small_mixed(50, batch=6, max_cached=1300, max_chunk=300, num_pages=48)
+    tick = DeviceTick(w, dtype, device)
+    tick.q.mul_(40)
+    ref, ref_lse = tick.oracle()
+    out, lse = tick.attend(exact_grid=True, return_lse=True)
+    compare(out, ref, what=f"large logits {dtype}")
+    assert np.isfinite(lse.cpu().numpy()).all()
+    assert np.abs(lse.cpu().numpy() - ref_lse).max() < 5e-3 * np.abs(ref_lse).max()
+
+
 def test_c2_decode_tick(device):
     say("c2 decode tick")
     w = synth.c2()
