@@ -247,7 +247,9 @@ __global__ __launch_bounds__(kLgThreads) void argmax_reduce_kernel(
     best = max_u64(max_u64(s_best[0], s_best[1]), max_u64(s_best[2], s_best[3]));
     const bool ok = row_ok[j] != 0 && best != 0;
     token_ids[j] = ok ? (int64_t)(0xFFFFFFFFu - (uint32_t)best) : -1;
-    if (max_logits != nullptr) max_logits[j] = ok ? key_value(best) : __builtin_nanf("");
+    // The quiet-NaN bits, stored as data: device code is built without NaN semantics,
+    // under which a NaN literal would be undefined.
+    if (max_logits != nullptr) max_logits[j] = ok ? key_value(best) : __uint_as_float(0x7FC00000u);
   }
 }
 
