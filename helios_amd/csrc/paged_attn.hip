@@ -44,7 +44,10 @@ constexpr int kPlanThreads = 1024;
 // workgroups, each row block's key tiles are cut into splits of at least
 // kMinSplitTiles tiles so that about kChunkFillWGs workgroups run; split partials are
 // merged by the combine kernel like decode splits.
-constexpr int kChunkFillWGs = 512;
+// 448: with one chunk workgroup per CU (228 VGPRs), fewer and longer splits than a
+// 512 target; the full-model tick measured 25.8-26.0 ms against 27.1-27.3 ms at 512
+// and 26.4-26.5 ms at 384, with the mixed tick unchanged.
+constexpr int kChunkFillWGs = 448;
 constexpr int kMinSplitTiles = 8;
 constexpr int kMaxChunkSplits = 64;
 constexpr int kCombRows = 8;  // output rows per combine record of a split chunk block
