@@ -43,11 +43,13 @@ constexpr int kPlanThreads = 1024;
 // Chunk split-K: when the chunk work items would launch fewer than kChunkFillWGs
 // workgroups, each row block's key tiles are cut into splits of at least
 // kMinSplitTiles tiles so that about kChunkFillWGs workgroups run; split partials are
-// merged by the combine kernel like decode splits.
-// 448: with one chunk workgroup per CU (228 VGPRs), fewer and longer splits than a
-// 512 target; the full-model tick measured 25.8-26.0 ms against 27.1-27.3 ms at 512
-// and 26.4-26.5 ms at 384, with the mixed tick unchanged.
-constexpr int kChunkFillWGs = 448;
+// merged by the combine kernel like decode splits. A CU holds one chunk workgroup
+// (228 VGPRs x 8 waves), so workgroups run in rounds of kChunkCUs: when rounding the
+// split count per block spills past whole rounds, the split size grows to the smallest
+// one that fits them (refine_split_tiles). On the full-model tick this took the 1024-row
+// chunk from about 550 workgroups (a third, partial round) to 512: 143 -> 110 us.
+constexpr int kChunkFillWGs = 512;
+constexpr int kChunkCUs = 256;  // CUs of an MI355X
 constexpr int kMinSplitTiles = 8;
 constexpr int kMaxChunkSplits = 64;
 constexpr int kCombRows = 8;  // output rows per combine record of a split chunk block
@@ -145,6 +147,29 @@ __host__ __device__ inline int chunk_split_count(int tiles, int split_tiles) {
   if (split_tiles <= 0 || tiles <= split_tiles) return 1;
   const int s = (tiles + split_tiles - 1) / split_tiles;
   return s < kMaxChunkSplits ? s : kMaxChunkSplits;
+}
+
+// Split size that keeps the chunk workgroups within whole rounds of kChunkCUs. wgs(st)
+// is the workgroup count at split size st (non-increasing in st); max_tiles is the
+// largest block's tile count (no block splits at that size). From st0, when wgs(st0)
+// spills past R >= 1 whole rounds, returns the smallest st whose count fits R rounds,
+// if one does; otherwise st0. The plan kernel and the host count call it with the same
+// counts, so both reach the same split size.
+template <typename WgsFn>
+__host__ __device__ inline int refine_split_tiles(int st0, int max_tiles, WgsFn wgs) {
+  if (st0 <= 0 || max_tiles <= st0) return st0;
+  const int64_t w0 = wgs(st0);
+  const int64_t rounds = w0 / kChunkCUs;
+  if (rounds < 1 || w0 % kChunkCUs == 0) return st0;
+  const int64_t target = rounds * kChunkCUs;
+  int lo = st0, hi = max_tiles;  // wgs(lo) > target
+  if (wgs(hi) > target) return st0;
+  while (hi - lo > 1) {
+    const int mid = lo + (hi - lo) / 2;
+    if (wgs(mid) <= target) hi = mid;
+    else lo = mid;
+  }
+  return hi;
 }
 
 // Decode key window of a one-token row at position L-1: keys [lo, L).
@@ -264,11 +289,15 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
   __syncthreads();
   int err = 0;
 
-  // Pass 1: chunk work before splitting (items and key tiles, head quads counted).
+  // Pass 1: chunk work before splitting (items and key tiles, head quads counted; the
+  // largest block's tiles).
+  __shared__ int max_blk_tiles;
+  if (threadIdx.x == 0) max_blk_tiles = 0;
+  __syncthreads();
   int64_t pf_items0 = 0, pf_tiles = 0;
   for (int b0 = 0; b0 < a.batch; b0 += kPlanThreads) {
     const int b = b0 + (int)threadIdx.x;
-    int items = 0, tiles = 0;
+    int items = 0, tiles = 0, tmax = 0;
     if (b < a.batch) {
       int e = 0;
       const SeqMeta m = plan_seq(a, b, e);
@@ -278,16 +307,43 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
           chunk_tiles(m.n, m.L, row0, a.rows_per_item, a.win_left, a.win_right, &tb, &te);
           tiles += (te - tb) * a.head_quads;
           items += a.head_quads;
+          tmax = max(tmax, te - tb);
         }
       }
     }
+    if (tmax > 0) atomicMax(&max_blk_tiles, tmax);  // LDS atomic
     int tot_i, tot_t;
     block_exclusive_scan(items, wave_tot, &tot_i);
     block_exclusive_scan(tiles, wave_tot, &tot_t);
     pf_items0 += tot_i;
     pf_tiles += tot_t;
   }
-  const int split_tiles = chunk_split_tiles(pf_tiles, pf_items0, a.hkv);
+  __syncthreads();
+  // Workgroups of the chunk launch at split size st (a block-wide pass; every thread
+  // runs it the same number of times, since the search depends only on block totals).
+  auto chunk_wgs = [&](int st) -> int64_t {
+    int64_t total = 0;
+    for (int b0 = 0; b0 < a.batch; b0 += kPlanThreads) {
+      const int b = b0 + (int)threadIdx.x;
+      int wg = 0;
+      if (b < a.batch) {
+        int e = 0;
+        const SeqMeta m = plan_seq(a, b, e);
+        if (m.n >= 2) {
+          for (int row0 = 0; row0 < m.n; row0 += a.rows_per_item) {
+            int tb, te;
+            chunk_tiles(m.n, m.L, row0, a.rows_per_item, a.win_left, a.win_right, &tb, &te);
+            wg += chunk_split_count(te - tb, st) * a.head_quads;
+          }
+        }
+      }
+      int tot;
+      block_exclusive_scan(wg, wave_tot, &tot);
+      total += tot;
+    }
+    return total * a.hkv;
+  };
+  const int split_tiles = refine_split_tiles(chunk_split_tiles(pf_tiles, pf_items0, a.hkv), max_blk_tiles, chunk_wgs);
 
   // Pass 2: work lists.
   int base_dec = 0, base_pf = 0, base_comb = 0, base_slot = 0;
@@ -1282,6 +1338,7 @@ int hx_varlen_attn_count_items(const int32_t* q_lens, const int32_t* k_lens, int
   const Geometry geo = geometry(n_q_heads, n_kv_heads);
   // Same two passes as plan_kernel: chunk items and tiles unsplit, then the split.
   int64_t items0 = 0, tiles0 = 0;
+  int max_tiles = 0;
   for (int b = 0; b < batch; ++b) {
     const int n = q_lens[b], L = k_lens[b];
     if (n < 0 || L < 0) return HX_E_INVALID_ARG;
@@ -1291,9 +1348,23 @@ int hx_varlen_attn_count_items(const int32_t* q_lens, const int32_t* k_lens, int
       chunk_tiles(n, L, row0, geo.rows_per_item, window_left, window_right, &tb, &te);
       tiles0 += (int64_t)(te - tb) * geo.head_quads;
       items0 += geo.head_quads;
+      max_tiles = te - tb > max_tiles ? te - tb : max_tiles;
     }
   }
-  const int split_tiles = chunk_split_tiles(tiles0, items0, n_kv_heads);
+  auto chunk_wgs = [&](int st) -> int64_t {
+    int64_t total = 0;
+    for (int b = 0; b < batch; ++b) {
+      const int n = q_lens[b], L = k_lens[b];
+      if (n < 2) continue;
+      for (int row0 = 0; row0 < n; row0 += geo.rows_per_item) {
+        int tb, te;
+        chunk_tiles(n, L, row0, geo.rows_per_item, window_left, window_right, &tb, &te);
+        total += (int64_t)chunk_split_count(te - tb, st) * geo.head_quads;
+      }
+    }
+    return total * n_kv_heads;
+  };
+  const int split_tiles = refine_split_tiles(chunk_split_tiles(tiles0, items0, n_kv_heads), max_tiles, chunk_wgs);
   int64_t nd = 0, np = 0, nc = 0;
   for (int b = 0; b < batch; ++b) {
     const int n = q_lens[b], L = k_lens[b];

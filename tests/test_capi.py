@@ -49,7 +49,9 @@ def _expected_counts(w: synth.Workload, window=(-1, 0)):
     """Work items from the closed forms: decode rows split keys in 256s; chunk rows go in
     blocks of rows_per_item, and when the unsplit blocks launch fewer than 512 workgroups
     each block's 64-key tiles are cut into splits of at least max(8, ceil(tiles * Hkv /
-    512)) tiles, every split row adding one combine record."""
+    512)) tiles, every split row adding one combine record. When the split workgroups
+    spill past R >= 1 whole rounds of 256 (one chunk workgroup per CU), the split size is
+    the smallest one, up to the largest block's tiles, whose count fits R rounds."""
     nd = nc = npf = 0
     G = w.n_q_heads // w.n_kv_heads
     gw = min(G, 4)
@@ -69,6 +71,18 @@ def _expected_counts(w: synth.Workload, window=(-1, 0)):
     split = 0
     if items0 and items0 * w.n_kv_heads < 512:
         split = max(8, -(-tiles0 * w.n_kv_heads // 512))
+
+    def split_count(t, st):
+        return 1 if not st or t <= st else min(64, -(-t // st))
+
+    def wgs(st):
+        return w.n_kv_heads * quads * sum(split_count(tiles(*blk), st) for blk in blocks)
+
+    if split:
+        w0 = wgs(split)
+        rounds, max_t = w0 // 256, max(tiles(*blk) for blk in blocks)
+        if rounds >= 1 and w0 % 256 and max_t > split and wgs(max_t) <= rounds * 256:
+            split = min(st for st in range(split, max_t + 1) if wgs(st) <= rounds * 256)
     for n, L in zip(w.q_lens, w.k_lens):
         if n == 1:
             lo = 0 if window[0] < 0 else max(0, L - 1 - window[0])
@@ -77,7 +91,7 @@ def _expected_counts(w: synth.Workload, window=(-1, 0)):
             nc += splits > 1
     for n, L, r0 in blocks:
         t = tiles(n, L, r0)
-        s = 1 if not split or t <= split else min(64, -(-t // split))
+        s = split_count(t, split)
         npf += s * quads
         if s > 1:
             nc += -(-min(rows_per_item, n - r0) // 8)  # combine records of up to 8 rows
@@ -88,6 +102,23 @@ def _expected_counts(w: synth.Workload, window=(-1, 0)):
 def test_count_items_matches_closed_form(name):
     w = getattr(synth, name)()
     assert ops.count_items(w.q_lens, w.k_lens, 32, 8, (-1, 0)) == _expected_counts(w)
+
+
+@pytest.mark.parametrize("chunks", [[(1024, 5120)], [(2048, 2048)], [(2048, 6144)], [(1536, 4096)],
+                                    [(3000, 3000)], [(512, 8192)], [(768, 3000)],
+                                    [(1024, 1024), (992, 1504)]])
+def test_chunk_splits_fill_whole_rounds(chunks):
+    """Chunk splits whose per-block rounding would spill into a partial extra round of
+    256 workgroups get the smallest larger split size that fits the whole rounds."""
+    q_lens = [n for n, _ in chunks] + [1] * 4
+    k_lens = [L for _, L in chunks] + [700, 1300, 257, 4096]
+    w = synth.Workload("rounds", q_lens, [L - n for n, L in zip(q_lens, k_lens)],
+                       [[0] * (-(-L // 256)) for L in k_lens], 64)
+    counts = ops.count_items(q_lens, k_lens, 32, 8, (-1, 0))
+    assert counts == _expected_counts(w)
+    # Without the refinement most of these spill to 536-696 workgroups (a partial third
+    # round); with it every one fits two rounds.
+    assert counts[1] * 8 <= 512
 
 
 def test_count_items_windows_and_groups():
