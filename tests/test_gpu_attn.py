@@ -131,6 +131,31 @@ def test_c4_long_context_shared_prefix(device):
     compare(out, ref, what="c4 (decoders + 192 chunk rows)", rows=rows)
 
 
+def test_chunk_splits_refined_to_whole_rounds(device):
+    """A 1536-row chunk over 4096 keys plus four decoders: the first split size spills
+    into a partial third round of 256 workgroups, so the plan grows it (host count and
+    plan kernel alike: the exact-hint launch reports no grid error). Sampled chunk rows
+    and every decoder against the oracle."""
+    say("refined chunk splits")
+    q_lens = [1536, 1, 1, 1, 1]
+    k_lens = [4096, 700, 1300, 257, 4096]
+    rng = np.random.default_rng(12)
+    pages = sum(-(-L // 256) for L in k_lens)
+    perm = [int(p) for p in rng.permutation(pages + 8)]
+    tables, i = [], 0
+    for L in k_lens:
+        tables.append(perm[i:i + -(-L // 256)])
+        i += -(-L // 256)
+    w = synth.Workload("refined", q_lens, [L - n for n, L in zip(q_lens, k_lens)], tables, pages + 8, seed=12)
+    assert ops.count_items(q_lens, k_lens, 32, 8, (-1, 0))[1] * 8 <= 512
+    tick = DeviceTick(w, torch.bfloat16, device, pool_on_device=True)
+    out = tick.attend(exact_grid=True)  # asserts the plan's error word is 0
+    sample = list(range(0, 48)) + list(range(744, 792)) + list(range(1488, 1536))
+    ref, _ = tick.oracle(rows={0: sample} | {b: [0] for b in range(1, 5)})
+    rows = np.array(sample + [1536 + b for b in range(4)])
+    compare(out, ref, what="refined splits (decoders + 144 chunk rows)", rows=rows)
+
+
 def test_deterministic_across_runs(device):
     say("determinism")
     w = synth.small_mixed(44, batch=8, max_cached=3000, max_chunk=500, num_pages=96)
