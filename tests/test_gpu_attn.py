@@ -156,6 +156,37 @@ def test_chunk_splits_refined_to_whole_rounds(device):
     compare(out, ref, what="refined splits (decoders + 144 chunk rows)", rows=rows)
 
 
+def test_graph_replay_matches_eager(device):
+    """One layer of a mixed tick (append of the new rows, decode splits, chunk rows,
+    combine) captured in a HIP graph and replayed three times, with eager launches and
+    a fill of the output between replays: every replay gives the eager bits. The path
+    records no memset and no host synchronisation."""
+    say("graph replay")
+    w = synth.small_mixed(61, batch=7, max_cached=1500, max_chunk=300, num_pages=64)
+    tick = DeviceTick(w, torch.bfloat16, device)
+    plan = ops.VarlenAttnPlan(
+        tick.cu_seq_q, tick.cu_seq_k, tick.seqused_k, total_q=w.total_q, max_q=w.max_q,
+        max_k=w.max_k, n_q_heads=w.n_q_heads, n_kv_heads=w.n_kv_heads, head_dim=w.head_dim,
+        page_size=w.page_size, block_table_stride=tick.block_table.shape[1], window=(-1, 0),
+        q_lens=w.q_lens, k_lens=w.k_lens)
+    append = (tick.k_new, tick.v_new, tick.write_slots)  # rows already in the pool: idempotent
+    eager = plan.run(tick.q, tick.k_pool, tick.v_pool, tick.block_table, append=append).clone()
+    out = torch.empty_like(eager)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.run(tick.q, tick.k_pool, tick.v_pool, tick.block_table, out=out, append=append)
+    for _ in range(3):
+        out.fill_(0)
+        graph.replay()
+        other = plan.run(tick.q, tick.k_pool, tick.v_pool, tick.block_table)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
+        assert torch.equal(other.view(torch.int16), eager.view(torch.int16))
+    assert plan.error_word() == 0
+    del graph
+
+
 def test_deterministic_across_runs(device):
     say("determinism")
     w = synth.small_mixed(44, batch=8, max_cached=3000, max_chunk=500, num_pages=96)
