@@ -16,8 +16,8 @@ from tests.gpu_cases import MAX_ABS, MEAN_ABS, say
 pytestmark = pytest.mark.gpu
 
 
-def _pool(device, pages=96, seed=3):
-    config = Qwen3Config(context_length=8192, n_layers=2, dtype=torch.bfloat16)
+def _pool(device, pages=96, seed=3, dtype=torch.bfloat16):
+    config = Qwen3Config(context_length=8192, n_layers=2, dtype=dtype)
     pool = KVPagePool(config, pages, device=device)
     g = torch.Generator(device=device).manual_seed(seed)
     for t in pool.keys + pool.values:
@@ -81,25 +81,26 @@ def test_levels_follow_shared_pages(device, always_cascade):
     assert levels[-1][2] == 8 and levels[-1][3] == [1, 3]
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("counts_kind", ["decode", "mixed"])
-def test_cascade_matches_oracle_and_plain_path(device, counts_kind, always_cascade):
-    say("cascade", counts_kind)
+def test_cascade_matches_oracle_and_plain_path(device, counts_kind, dtype, always_cascade):
+    say("cascade", counts_kind, dtype)
     cached = [2100, 2300, 300, 2100, 1700, 520, 2048, 900, 2800]
     counts = [1] * len(cached)
     if counts_kind == "mixed":
         counts[2] = 130  # a chunk row block next to the decode rows
     outs = []
     for cascade in (True, False):
-        pool = _pool(device)
+        pool = _pool(device, dtype=dtype)
         _, caches = _shared_caches(pool, cached)
         batch = PackedBatchCache(caches, prefix_cascade=cascade)
         batch.prepare_packed(counts)
         assert (batch._cascade is not None) == cascade
         total = sum(counts)
         g = torch.Generator(device=device).manual_seed(11)
-        q = torch.randn((1, 32, total, 128), generator=g, device=device).to(torch.bfloat16)
-        k = torch.randn((1, 8, total, 128), generator=g, device=device).to(torch.bfloat16)
-        v = torch.randn((1, 8, total, 128), generator=g, device=device).to(torch.bfloat16)
+        q = torch.randn((1, 32, total, 128), generator=g, device=device).to(dtype)
+        k = torch.randn((1, 8, total, 128), generator=g, device=device).to(dtype)
+        v = torch.randn((1, 8, total, 128), generator=g, device=device).to(dtype)
         out = batch.attend(0, q, k, v)
         torch.cuda.synchronize()
         want = _oracle(pool, caches, counts, q[0].transpose(0, 1))
