@@ -16,8 +16,8 @@ from tests.gpu_cases import MAX_ABS, MEAN_ABS, say
 pytestmark = pytest.mark.gpu
 
 
-def _pool(device, pages=96, seed=3, dtype=torch.bfloat16):
-    config = Qwen3Config(context_length=8192, n_layers=2, dtype=dtype)
+def _pool(device, pages=96, seed=3, dtype=torch.bfloat16, n_heads=32, n_kv_heads=8):
+    config = Qwen3Config(context_length=8192, n_layers=2, dtype=dtype, n_heads=n_heads, n_kv_heads=n_kv_heads)
     pool = KVPagePool(config, pages, device=device)
     g = torch.Generator(device=device).manual_seed(seed)
     for t in pool.keys + pool.values:
@@ -109,6 +109,28 @@ def test_cascade_matches_oracle_and_plain_path(device, counts_kind, dtype, alway
         outs.append(got)
         batch.advance_packed()
     _compare(outs[0], outs[1], "cascade vs plain")
+
+
+@pytest.mark.parametrize("n_heads,n_kv_heads", [(64, 8), (16, 8)])
+def test_cascade_other_group_sizes(device, n_heads, n_kv_heads, always_cascade):
+    """G = 8 (the level batch runs two head quads per KV head) and G = 2."""
+    say("cascade group", n_heads, n_kv_heads)
+    cached = [2100, 2300, 300, 2100, 1700, 520]
+    counts = [1, 1, 90, 1, 1, 1]
+    pool = _pool(device, n_heads=n_heads, n_kv_heads=n_kv_heads)
+    _, caches = _shared_caches(pool, cached)
+    batch = PackedBatchCache(caches, prefix_cascade=True)
+    batch.prepare_packed(counts)
+    assert batch._cascade is not None
+    total = sum(counts)
+    g = torch.Generator(device=device).manual_seed(12)
+    q = torch.randn((1, n_heads, total, 128), generator=g, device=device).to(torch.bfloat16)
+    k = torch.randn((1, n_kv_heads, total, 128), generator=g, device=device).to(torch.bfloat16)
+    v = torch.randn((1, n_kv_heads, total, 128), generator=g, device=device).to(torch.bfloat16)
+    out = batch.attend(0, q, k, v)
+    torch.cuda.synchronize()
+    want = _oracle(pool, caches, counts, q[0].transpose(0, 1))
+    _compare(out[0].transpose(0, 1).float().cpu().numpy(), want, f"cascade G={n_heads // n_kv_heads}")
 
 
 def test_uniform_decode_cascade_over_ticks(device, always_cascade):
