@@ -88,6 +88,38 @@ def test_kernel_matches_oracle_and_reference_ops(device, dtype, rows, offset):
     assert torch.equal(vf[untouched].view(torch.int16), vb[untouched].view(torch.int16))
 
 
+@pytest.mark.parametrize("hq,hkv", [(64, 8), (16, 2), (8, 8)])
+def test_kernel_other_head_counts(device, hq, hkv):
+    """Head counts whose last 4-head group is partial (16 + 2 * 2 = 20 heads) or that
+    take more passes per row (64 + 16 = 80 heads), both layouts."""
+    say("qk rope heads", hq, hkv)
+    g = torch.Generator(device="cpu").manual_seed(hq + hkv)
+    d, rows = 128, 37
+    for offset in (0, 1):
+        proj = torch.randn(rows, (hq + 2 * hkv) * d + offset, generator=g).to(torch.bfloat16).to(device)[:, offset:]
+        q = proj[:, : hq * d].view(rows, hq, d)
+        k = proj[:, hq * d:(hq + hkv) * d].view(rows, hkv, d)
+        v = proj[:, (hq + hkv) * d:].view(rows, hkv, d)
+        wq = (1 + 0.2 * torch.randn(d, generator=g)).float().to(device)
+        wk = (1 + 0.2 * torch.randn(d, generator=g)).float().to(device)
+        cos, sin = dense_torch.rope_parameters(d, 4096, 1_000_000.0)
+        cos, sin = cos.to(device), sin.to(device)
+        positions = torch.randint(0, 4096, (rows,), generator=g).to(device)
+        k_pool = torch.zeros(2, 256, hkv, d, dtype=torch.bfloat16, device=device)
+        v_pool = torch.zeros_like(k_pool)
+        slots = torch.randperm(512, generator=g)[:rows].to(device)
+        q_out = ops.qk_norm_rope_append(q, k, v, wq, wk, cos, sin, positions, k_pool, v_pool, slots, 1e-6)
+        torch.cuda.synchronize()
+
+        def ref(x, w):
+            y = dense_torch.rms_norm(x.transpose(0, 1).unsqueeze(0), w, 1e-6)
+            return dense_torch.apply_rope(y, cos, sin, positions.unsqueeze(0))[0].transpose(0, 1)
+
+        assert pair_close(q_out, ref(q, wq))
+        assert pair_close(k_pool.view(-1, hkv, d)[slots], ref(k, wk))
+        assert torch.equal(v_pool.view(-1, hkv, d)[slots].view(torch.int16), v.contiguous().view(torch.int16))
+
+
 def test_attend_projected_matches_torch_norm_rope_then_attend(device):
     say("attend_projected")
     config = Qwen3Config(context_length=8192, n_layers=2, dtype=torch.bfloat16)
