@@ -12,6 +12,8 @@ LIBRARY_PATH = Path(__file__).resolve().with_name("libhelios_paged.so")
 HEADER_PATH = Path(__file__).resolve().parent.parent / "include" / "helios_paged.h"
 
 HX_OK = 0
+# hx_abi_version() of the library these signatures describe (bumped on any signature change).
+ABI_VERSION = 2
 HX_E_INVALID_ARG = -1
 HX_E_UNSUPPORTED = -2
 HX_E_WORKSPACE = -3
@@ -170,6 +172,12 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = restype
             fn.argtypes = argtypes
+        found = handle.hx_abi_version()
+        if found != ABI_VERSION:
+            raise HeliosLibraryError(
+                f"{LIBRARY_PATH.name} has ABI version {found}, these bindings expect "
+                f"{ABI_VERSION}; rebuild it with `python -m helios_amd.build`."
+            )
         _lib = handle
     return _lib
 

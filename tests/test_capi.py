@@ -25,8 +25,15 @@ def test_library_exports_every_header_function():
     assert set(names) <= exported
 
 
+def test_loader_rejects_a_library_of_another_abi_version(monkeypatch):
+    monkeypatch.setattr(_capi, "_lib", None)
+    monkeypatch.setattr(_capi, "ABI_VERSION", _capi.ABI_VERSION + 1)
+    with pytest.raises(_capi.HeliosLibraryError, match="ABI version"):
+        _capi.lib()
+
+
 def test_abi_version_and_strerror():
-    assert _capi.lib().hx_abi_version() == 2
+    assert _capi.lib().hx_abi_version() == _capi.ABI_VERSION == 2
     assert _capi.strerror(0) == "success"
     assert "invalid" in _capi.strerror(_capi.HX_E_INVALID_ARG)
     with pytest.raises(ValueError):
