@@ -298,8 +298,8 @@ def long_context(device, steps: int = 10, warmup: int = 3):
 
 
 def tick_metadata_leg(device, ticks: int = 20):
-    """Per-tick metadata of PackedBatchCache.prepare_packed: the reference's host lists
-    and pageable copies vs the metadata kernel, on the mixed tick (32 decoders + chunks
+    """Per-tick metadata of PackedBatchCache.prepare_packed: built on the host (numpy,
+    pageable copies) vs the metadata kernel, on the mixed tick (32 decoders + chunks
     of 1024 and 992) and on a 128-decoder + 1024-chunk tick (the full-model shape).
     Host time per prepare_packed call (what the scheduler thread waits for) and the
     kernel's own time."""
@@ -318,7 +318,7 @@ def tick_metadata_leg(device, ticks: int = 20):
     out = {}
     for name, (lengths, counts) in shapes.items():
         res = {"sequences": len(counts), "tokens": sum(counts)}
-        for mode in ("host_lists", "device_kernel"):
+        for mode in ("host_numpy", "device_kernel"):
             pages = sum(-(-(n + c * (ticks + 2)) // 256) for n, c in zip(lengths, counts)) + 8
             pool = KVPagePool(config, pages, device=device)
             caches = []
@@ -341,13 +341,14 @@ def tick_metadata_leg(device, ticks: int = 20):
             res[f"{mode}_us"] = round(statistics.median(times) * 1e6, 1)
             if mode == "device_kernel":
                 ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-                meta = batch._device_meta
+                batch.prepare_packed(counts)
+                seq = batch._device_meta.last["seq"]
                 ev[0].record()
                 from helios_amd import ops
-                ops.tick_metadata(meta.seq, meta.block_table, 256, total_q=sum(counts),
-                                  cu_seq_q=meta.cu_seq_q, cu_seq_k=meta.cu_seq_k,
-                                  seqused_k=meta.seqused_k, write_slots=meta.write_slots,
-                                  positions=meta.positions, logit_indices=meta.logit_indices,
+                ops.tick_metadata(seq, batch.block_table, 256, total_q=sum(counts),
+                                  cu_seq_q=batch.cu_seq_q, cu_seq_k=batch.cu_seq_k,
+                                  seqused_k=batch.seqused_k, write_slots=batch.write_slots,
+                                  positions=batch.positions[0], logit_indices=batch.logit_indices,
                                   n_logits=len(counts))
                 ev[1].record()
                 torch.cuda.synchronize()
@@ -491,40 +492,23 @@ def full_tick_leg(device, ticks: int = 4, seed: int = 5):
     whole tick and the attention step's share (q/k norm + RoPE + KV append + paged
     attention), for this build's path (metadata kernel, fused norm/RoPE/append,
     shared-prefix cascade, fused final-norm/logits/argmax) and for the reference's
-    sequence on the same attention kernels (host metadata lists, torch norm/RoPE,
+    sequence on the same attention kernels (host-built metadata, torch norm/RoPE,
     attend, every row reading its own prefix pages, bf16 logits then argmax)."""
-    import numpy as np
     import torch
 
+    from helios_amd import synth
     from helios_amd.config import Qwen3Config
     from helios_amd.decoder import PagedQwen3Decoder
-    from helios_amd.paged_cache import KVPagePool, PackedBatchCache, PagedKVCache
+    from helios_amd.paged_cache import KVPagePool, PackedBatchCache
 
     config = Qwen3Config()
-    rng = np.random.default_rng(seed)
-    ctx = [int(x) for x in rng.integers(1024, 8193, 128)]
-    prefix_pages = 16
-    own_pages = sum(-(-c // 256) - min(prefix_pages, (c - 1) // 256) + 1 for c in ctx) + 8
-    num_pages = prefix_pages + own_pages + 8
+    lengths, counts = synth.c5_lengths(seed)
+    ctx = lengths[:-1]
     model = PagedQwen3Decoder(config, device, seed=seed)
-    pool = KVPagePool(config, num_pages, device=device)
+    pool = KVPagePool(config, synth.c5_pool_pages(lengths, counts), device=device)
     g = torch.Generator(device=device).manual_seed(seed)
-    for t in pool.keys + pool.values:
-        t.normal_(generator=g)
-    prefix = PagedKVCache(pool, config.context_length)
-    prefix.pages.extend(pool.acquire(prefix_pages))
-    prefix.length = prefix_pages * 256
-    caches, lengths = [], []
-    for c in ctx + [None]:
-        cache = PagedKVCache(pool, config.context_length)
-        cached = c - 1 if c is not None else prefix.length
-        shared = min(prefix_pages, cached // 256)
-        cache.pages.extend(prefix.pages[:shared])
-        cache.pages.extend(pool.acquire(-(-cached // 256) - shared))
-        cache.length = cached
-        caches.append(cache)
-        lengths.append(cached)
-    counts = [1] * len(ctx) + [1024]
+    pool.storage.normal_(generator=g)
+    prefix, caches = synth.shared_prefix_caches(pool, lengths)
     tokens = sum(counts)
     input_ids = torch.randint(0, config.vocab_size, (1, tokens), generator=g, device=device)
 

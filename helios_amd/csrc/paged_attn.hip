@@ -16,9 +16,10 @@
 //                   softmax uses DPP wave reductions plus a 4-wave LDS step; PV runs on
 //                   VALU in fp32.
 //                   A sequence that fits one split writes its output directly; longer ones
-//                   write partials: fp32 (m, l) and o / l rounded to bf16 (the partial
-//                   stores cost more than their 1.6% of the bytes suggests, so they are
-//                   halved; the extra error is one more bf16 rounding of the output).
+//                   write partials: fp32 (m, l) and o / l rounded to the element type (the
+//                   partial stores cost more than their 1.6% of the bytes suggests, so they
+//                   are 16-bit; the extra error is one more rounding of the output in its
+//                   own precision).
 //   chunk_kernel    prefill chunks: 8 waves per workgroup (2 per SIMD), each wave owning
 //                   32 query rows of one head; 64-key K / V^T tiles go through LDS with a
 //                   register prefetch of the next tile; S^T = K Q^T and O^T = V^T P^T both
@@ -454,7 +455,7 @@ struct RunArgs {
   const int4* pf_items;
   const int32_t* pf_base;  // per chunk item: first partial row of its block (split blocks)
   float2* part_ml;   // per (slot, head): running max m (log2 units) and sum l
-  uint16_t* part_o;  // per (slot, head, dim): o / l as bf16
+  uint16_t* part_o;  // per (slot, head, dim): o / l in the element type T
   int64_t dec_cap;   // decode slots [0, dec_cap); chunk split rows follow
   int64_t slot_cap;  // all partial slots
   int64_t q_row, q_head;     // element strides
@@ -672,9 +673,14 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
         *reinterpret_cast<uint4*>(const_cast<uint8_t*>(a.v) + off * (int64_t)sizeof(T)) = vnew;
       }
     }
+    // When the new token is the split's only visible key (nfirst == nn), every masked
+    // row re-read that token's pool row, which this launch has not written yet: stale
+    // page contents, possibly not finite, that p = 0 would turn into NaN. All rows take
+    // the new token's values instead (masked rows need any finite data).
+    const bool alone = nfirst == nn;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      if (i == i_new && owner) {
+      if (alone || (i == i_new && owner)) {
         kr[i] = knew;
         vr[i] = vnew;
       }
@@ -783,7 +789,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
       if (a.lse && d == 0)
         a.lse[(int64_t)qh * a.total_q + q0] = lh > 0.f ? (mh + log2f(lh)) * kLn2 : -INFINITY;
     } else {
-      a.part_o[((int64_t)item * a.hq + qh) * kD + d] = hx::Elem<__bf16>::bits(lh > 0.f ? acc / lh : 0.f);
+      a.part_o[((int64_t)item * a.hq + qh) * kD + d] = E::bits(lh > 0.f ? acc / lh : 0.f);
       if (d == 0) a.part_ml[(int64_t)item * a.hq + qh] = make_float2(mh, lh);
     }
   }
@@ -810,7 +816,7 @@ struct CombAcc {
 // Merges the partials of splits [s0, s_end), s_end - s0 <= NC, into r: the NC (m, l)
 // pairs and partial rows are loaded together (indices past s_end re-read s_end - 1 and
 // get weight 0).
-template <int NC>
+template <typename T, int NC>
 __device__ __forceinline__ void combine_step(const float2* ml, const uint16_t* po, int64_t step_ml,
                                              int64_t step_o, int s0, int s_end, CombAcc& r) {
   float2 mlv[NC];
@@ -838,8 +844,8 @@ __device__ __forceinline__ void combine_step(const float2* ml, const uint16_t* p
     const uint32_t w4[4] = {ov[j].x, ov[j].y, ov[j].z, ov[j].w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      r.acc[2 * e] += wgt * hx::Elem<__bf16>::lo(w4[e]);
-      r.acc[2 * e + 1] += wgt * hx::Elem<__bf16>::hi(w4[e]);
+      r.acc[2 * e] += wgt * hx::Elem<T>::lo(w4[e]);
+      r.acc[2 * e + 1] += wgt * hx::Elem<T>::hi(w4[e]);
     }
   }
   r.m = cm;
@@ -850,6 +856,7 @@ __device__ __forceinline__ void combine_step(const float2* ml, const uint16_t* p
 // output is acc / l. Groups of kCombChunk while more than four splits remain (the last
 // of them may re-read clamped entries), then one group of four or two: records of up to
 // four splits load no more than the next power of two.
+template <typename T>
 __device__ __forceinline__ CombAcc combine_range(const RunArgs& a, int64_t base, int qh, int ch,
                                                  int s_lo, int s_hi) {
   const float2* ml = a.part_ml + base * a.hq + qh;
@@ -861,11 +868,11 @@ __device__ __forceinline__ CombAcc combine_range(const RunArgs& a, int64_t base,
 #pragma unroll
   for (int e = 0; e < 8; ++e) r.acc[e] = 0.f;
   int s0 = s_lo;
-  for (; s_hi - s0 > 4; s0 += kCombChunk) combine_step<kCombChunk>(ml, po, a.hq, step_o, s0, min(s_hi, s0 + kCombChunk), r);
+  for (; s_hi - s0 > 4; s0 += kCombChunk) combine_step<T, kCombChunk>(ml, po, a.hq, step_o, s0, min(s_hi, s0 + kCombChunk), r);
   if (s_hi - s0 > 2)
-    combine_step<4>(ml, po, a.hq, step_o, s0, s_hi, r);
+    combine_step<T, 4>(ml, po, a.hq, step_o, s0, s_hi, r);
   else if (s_hi > s0)
-    combine_step<2>(ml, po, a.hq, step_o, s0, s_hi, r);
+    combine_step<T, 2>(ml, po, a.hq, step_o, s0, s_hi, r);
   return r;
 }
 
@@ -908,7 +915,7 @@ __global__ __launch_bounds__(kCombThreads, 4) void combine_kernel(RunArgs a) {
     for (int t = threadIdx.x; t < tasks; t += kCombThreads) {
       const int r = t / kPerRow;
       const int h = (t - r * kPerRow) >> 4, ch = t & 15;
-      const CombAcc res = combine_range(a, (int64_t)first + (int64_t)r * splits, g * G + h, ch, 0, splits);
+      const CombAcc res = combine_range<T>(a, (int64_t)first + (int64_t)r * splits, g * G + h, ch, 0, splits);
       combine_store<T>(a, res, q0 + r, g * G + h, ch);
     }
     return;
@@ -921,7 +928,7 @@ __global__ __launch_bounds__(kCombThreads, 4) void combine_kernel(RunArgs a) {
   const int span = (splits + ranges - 1) / ranges;
   if (rg < ranges) {
     const int s_lo = min(splits, rg * span), s_hi = min(splits, s_lo + span);
-    const CombAcc res = combine_range(a, (int64_t)first + (int64_t)r * splits, g * G + h, ch, s_lo, s_hi);
+    const CombAcc res = combine_range<T>(a, (int64_t)first + (int64_t)r * splits, g * G + h, ch, s_lo, s_hi);
     sh[0][t] = res.m;
     sh[1][t] = res.l;
 #pragma unroll
@@ -1255,8 +1262,8 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
           const int d0 = 16 * db + 4 * (lane >> 4);
-          const uint2 u = make_uint2(hx::pack2_round<__bf16>(oacc[db][rb][0] * inv, oacc[db][rb][1] * inv),
-                                     hx::pack2_round<__bf16>(oacc[db][rb][2] * inv, oacc[db][rb][3] * inv));
+          const uint2 u = make_uint2(hx::pack2_round<T>(oacc[db][rb][0] * inv, oacc[db][rb][1] * inv),
+                                     hx::pack2_round<T>(oacc[db][rb][2] * inv, oacc[db][rb][3] * inv));
           *reinterpret_cast<uint2*>(prow + d0) = u;
         }
         if ((lane >> 4) == 0)
@@ -1539,6 +1546,11 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (app != nullptr && total_q > 0) {
     if (!app->k_new || !app->v_new || !app->write_slots) return HX_E_INVALID_ARG;
+    // Write slots index pool rows of n_kv_heads * head_dim contiguous elements (the pool
+    // layout of the reference, [pages, page_size, n_kv_heads, head_dim] contiguous); the
+    // append kernel and the attention kernels must agree on that row address.
+    if (kv_row_stride != (int64_t)n_kv_heads * head_dim || kv_head_stride != head_dim) return HX_E_INVALID_ARG;
+    if (page_size > 0 && app->pool_rows != (int64_t)num_pages * page_size) return HX_E_INVALID_ARG;
     if ((uintptr_t)app->k_new % 16 || (uintptr_t)app->v_new % 16 || app->kn_row % 8 ||
         app->kn_head % 8 || app->vn_row % 8 || app->vn_head % 8 || app->kn_row < 0 ||
         app->kn_head < 0 || app->vn_row < 0 || app->vn_head < 0 || app->pool_rows < 0)

@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 from collections.abc import Sequence
 from typing import NamedTuple
 
@@ -26,6 +27,28 @@ import torch
 from helios_amd import _capi
 
 _SUPPORTED = {torch.bfloat16: _capi.HX_DTYPE_BF16, torch.float16: _capi.HX_DTYPE_FP16}
+
+# With HELIOS_AMD_CHECK_ERRORS=1 every attention run synchronises and raises RuntimeError
+# when the kernels flagged bad metadata (a page id outside the pool, a length clamped to
+# max_k / max_q / the table width, a malformed cu_seq_q, or a plan / run mismatch). Off by
+# default: reading the flag is a device-to-host round trip per call, and the reference's
+# hot path never synchronises (tests/test_continuous_batching.py:499-518). The kernels
+# never read or write out of bounds either way.
+CHECK_ERRORS = os.environ.get("HELIOS_AMD_CHECK_ERRORS", "") not in ("", "0")
+
+_WERR_TEXT = {
+    _capi.HX_WERR_BAD_PAGE: "a block-table page id outside the pool",
+    _capi.HX_WERR_CLAMPED_LEN: "a sequence length beyond max_k, max_q or the block table",
+    _capi.HX_WERR_BAD_CU_SEQ: "cu_seq_q not monotone or beyond the query rows",
+    _capi.HX_WERR_GRID: "more work items than the launch grid covered",
+    _capi.HX_WERR_PLAN_MISMATCH: "a run whose shape differs from its plan",
+}
+
+
+def describe_error_word(word: int) -> str:
+    """Text for the HX_WERR_* bits of an attention workspace error word."""
+    parts = [text for bit, text in _WERR_TEXT.items() if word & bit]
+    return "; ".join(parts) if parts else "no error"
 
 
 class AuxRequest(NamedTuple):
@@ -536,6 +559,12 @@ class VarlenAttnPlan:
         off = self._ws_offset + _capi.lib().hx_varlen_attn_error_word_offset()
         return int(self.workspace[off:off + 4].view(torch.int32).item())
 
+    def check_errors(self) -> None:
+        """Raise RuntimeError if the plan or a run flagged bad metadata (synchronises)."""
+        word = self.error_word()
+        if word:
+            raise RuntimeError(f"paged attention metadata error {word:#x}: {describe_error_word(word)}")
+
     def run(
         self,
         query: torch.Tensor,
@@ -646,6 +675,8 @@ class VarlenAttnPlan:
                 slots.data_ptr(), pool_rows,
                 *hints, self.ws_ptr, self.ws_bytes, _stream_ptr(query.device))
             _capi.check(code, "hx_varlen_attn_append_run")
+        if CHECK_ERRORS:
+            self.check_errors()
         return (out, lse) if return_lse else out
 
 

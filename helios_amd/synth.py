@@ -12,6 +12,9 @@ Workloads (the five benchmark configurations):
   c3  32 decode sequences (cached 1k-4k) + chunks of 1024 tokens at 0 and 992 at 512.
   c4  8 decode sequences at 32768 keys whose first 16 pages are shared, + a
       4096-token chunk at positions 4096-8191 whose first 16 pages are a copy.
+  c5  (request caches on a real pool) 128 decoders, contexts uniform in [1024, 8192],
+      each holding min(16, cached // 256) pages of one 4096-token prefix, + one
+      request that has cached that prefix and prefills a 1024-token chunk.
 """
 
 from __future__ import annotations
@@ -265,3 +268,49 @@ def host_inputs(w: Workload, dtype=np.float32) -> dict[str, np.ndarray]:
         "k_pool": normal(s + 4, (w.num_pages, w.page_size, w.n_kv_heads, w.head_dim), dtype),
         "v_pool": normal(s + 5, (w.num_pages, w.page_size, w.n_kv_heads, w.head_dim), dtype),
     }
+
+
+# ----------------------------------------------------------------- c5: request caches
+C5_PREFIX_PAGES = 16
+
+
+def c5_lengths(seed: int = 5, decoders: int = 128, chunk: int = 1024,
+               prefix_pages: int = C5_PREFIX_PAGES) -> tuple[list[int], list[int]]:
+    """Cached lengths and tokens this tick of the full-model tick: ``decoders`` requests
+    whose contexts are uniform in [1024, 8192] (cached = context - 1, one decode token)
+    and one request that has cached the whole prefix and prefills ``chunk`` tokens."""
+    rng = np.random.default_rng(seed)
+    contexts = [int(x) for x in rng.integers(1024, 8193, decoders)]
+    return [c - 1 for c in contexts] + [prefix_pages * 256], [1] * decoders + [chunk]
+
+
+def c5_pool_pages(lengths: list[int], counts: list[int], prefix_pages: int = C5_PREFIX_PAGES,
+                  page_size: int = 256) -> int:
+    """Pool pages the tick needs: the prefix, each request's own pages after the tick,
+    and one spare page per request (a tick that crosses a page boundary)."""
+    own = sum(-(-(n + c) // page_size) - min(prefix_pages, n // page_size) + 1
+              for n, c in zip(lengths, counts))
+    return prefix_pages + own + 8
+
+
+def shared_prefix_caches(pool, lengths: list[int], prefix_pages: int = C5_PREFIX_PAGES):
+    """A prefix request of ``prefix_pages`` full pages and one request cache per entry of
+    ``lengths`` that holds min(prefix_pages, length // page_size) of its pages (the same
+    page handles, as a prefix-cache restore leaves them) and owns the rest. Page
+    contents are whatever the pool holds. Returns (prefix, caches)."""
+    from helios_amd.paged_cache import PagedKVCache
+
+    size = pool.page_size
+    limit = pool.config.context_length
+    prefix = PagedKVCache(pool, limit)
+    prefix.pages.extend(pool.acquire(prefix_pages))
+    prefix.length = prefix_pages * size
+    caches = []
+    for n in lengths:
+        cache = PagedKVCache(pool, limit)
+        shared = min(prefix_pages, n // size)
+        cache.pages.extend(prefix.pages[:shared])
+        cache.pages.extend(pool.acquire(-(-n // size) - shared))
+        cache.length = n
+        caches.append(cache)
+    return prefix, caches

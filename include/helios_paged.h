@@ -187,7 +187,10 @@ int hx_varlen_attn_run(const void* q, int64_t q_row_stride, int64_t q_head_strid
  * launch; when chunk rows are present every row is appended first by the append
  * kernel. The pool must hold the token of decode row b at block-table position
  * seqused_k[b] - 1, i.e. write_slots must agree with the block table, as the
- * reference's metadata does by construction. pool_rows = num_pages * page_size.
+ * reference's metadata does by construction. pool_rows = num_pages * page_size. The
+ * pools must be contiguous rows: kv_row_stride == n_kv_heads * head_dim and
+ * kv_head_stride == head_dim (HX_E_INVALID_ARG otherwise), since a write slot names a
+ * whole pool row.
  */
 int hx_varlen_attn_append_run(const void* q, int64_t q_row_stride, int64_t q_head_stride,
                               void* k_cache, void* v_cache,

@@ -12,8 +12,19 @@ from helios_amd import ops, synth
 from oracle import attention as oa
 from oracle import kv_bytes
 
-MAX_ABS = 2e-2   # tolerance of bf16/fp16 attention output vs the fp64 oracle (max |err|)
+MAX_ABS = 2e-2   # tolerance of bf16 attention output vs the fp64 oracle (max |err|)
 MEAN_ABS = 2e-3  # and mean |err|
+# fp16 carries 3 more mantissa bits than bf16, so its bound is 8x tighter at the same
+# headroom over one rounding of the output (|o| up to about 4 in these cases). Split
+# partials stored in bf16 for an fp16 run (an 8-bit mantissa) exceed it on
+# sharp-softmax rows, where the output is a single V row.
+FP16_MAX_ABS = 4e-3
+FP16_MEAN_ABS = 3e-4
+
+
+def tolerance(dtype: torch.dtype) -> tuple[float, float]:
+    """(max-abs, mean-abs) bound of attention output in ``dtype`` against the oracle."""
+    return (FP16_MAX_ABS, FP16_MEAN_ABS) if dtype == torch.float16 else (MAX_ABS, MEAN_ABS)
 
 
 def say(*parts) -> None:
@@ -33,15 +44,8 @@ class DeviceTick:
         self.q = torch.from_numpy(synth.normal(s + 1, (T, w.n_q_heads, w.head_dim))).to(dtype).to(device)
         self.k_new = torch.from_numpy(synth.normal(s + 2, (T, w.n_kv_heads, w.head_dim))).to(dtype).to(device)
         self.v_new = torch.from_numpy(synth.normal(s + 3, (T, w.n_kv_heads, w.head_dim))).to(dtype).to(device)
-        shape = (w.num_pages, w.page_size, w.n_kv_heads, w.head_dim)
-        if pool_on_device:
-            g = torch.Generator(device=device)
-            g.manual_seed(s + 4)
-            self.k_pool = torch.randn(shape, generator=g, device=device, dtype=torch.float32).to(dtype)
-            self.v_pool = torch.randn(shape, generator=g, device=device, dtype=torch.float32).to(dtype)
-        else:
-            self.k_pool = torch.from_numpy(synth.normal(s + 4, shape)).to(dtype).to(device)
-            self.v_pool = torch.from_numpy(synth.normal(s + 5, shape)).to(dtype).to(device)
+        self.pool_on_device = pool_on_device
+        self.k_pool, self.v_pool = self.fresh_pools()
         self.block_table = torch.from_numpy(w.block_table()).to(device)
         self.cu_seq_q = torch.tensor(w.cu_seq_q, dtype=torch.int32, device=device)
         self.cu_seq_k = torch.tensor(w.cu_seq_k, dtype=torch.int32, device=device)
@@ -49,15 +53,32 @@ class DeviceTick:
         self.write_slots = torch.from_numpy(w.write_slots()).to(device)
         ops.kv_append(self.k_pool, self.v_pool, self.write_slots, self.k_new, self.v_new)
 
+    def fresh_pools(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """The tick's K and V pools before the append (the same bits every call)."""
+        w, s, dtype, device = self.w, self.w.seed * 7919, self.dtype, self.device
+        shape = (w.num_pages, w.page_size, w.n_kv_heads, w.head_dim)
+        if self.pool_on_device:
+            g = torch.Generator(device=device)
+            g.manual_seed(s + 4)
+            k = torch.randn(shape, generator=g, device=device, dtype=torch.float32).to(dtype)
+            v = torch.randn(shape, generator=g, device=device, dtype=torch.float32).to(dtype)
+            return k, v
+        return (torch.from_numpy(synth.normal(s + 4, shape)).to(dtype).to(device),
+                torch.from_numpy(synth.normal(s + 5, shape)).to(dtype).to(device))
+
+    def plan(self, *, window=(-1, 0)) -> ops.VarlenAttnPlan:
+        w = self.w
+        return ops.VarlenAttnPlan(
+            self.cu_seq_q, self.cu_seq_k, self.seqused_k, total_q=w.total_q, max_q=w.max_q,
+            max_k=w.max_k, n_q_heads=w.n_q_heads, n_kv_heads=w.n_kv_heads,
+            head_dim=w.head_dim, page_size=w.page_size,
+            block_table_stride=self.block_table.shape[1], window=window,
+            q_lens=w.q_lens, k_lens=w.k_lens)
+
     def attend(self, *, window=(-1, 0), exact_grid=False, return_lse=False):
         w = self.w
         if exact_grid:
-            plan = ops.VarlenAttnPlan(
-                self.cu_seq_q, self.cu_seq_k, self.seqused_k, total_q=w.total_q, max_q=w.max_q,
-                max_k=w.max_k, n_q_heads=w.n_q_heads, n_kv_heads=w.n_kv_heads,
-                head_dim=w.head_dim, page_size=w.page_size,
-                block_table_stride=self.block_table.shape[1], window=window,
-                q_lens=w.q_lens, k_lens=w.k_lens)
+            plan = self.plan(window=window)
             res = plan.run(self.q, self.k_pool, self.v_pool, self.block_table, return_lse=return_lse)
             assert plan.error_word() == 0
             return res
@@ -89,8 +110,12 @@ def host_append_reference(w: synth.Workload, dtype) -> dict[str, np.ndarray]:
     return xr
 
 
-def compare(got: torch.Tensor, ref: np.ndarray, *, what: str, max_abs=MAX_ABS, mean_abs=MEAN_ABS,
+def compare(got: torch.Tensor, ref: np.ndarray, *, what: str, max_abs=None, mean_abs=None,
             rows: np.ndarray | None = None) -> tuple[float, float]:
+    """Assert ``got`` is within the bound of its dtype (``tolerance``) of ``ref``."""
+    d_max, d_mean = tolerance(got.dtype)
+    max_abs = d_max if max_abs is None else max_abs
+    mean_abs = d_mean if mean_abs is None else mean_abs
     g = got.float().cpu().numpy().astype(np.float64)
     if rows is not None:
         g, ref = g[rows], ref[rows]

@@ -1,7 +1,7 @@
 """Paged varlen GQA attention on the GPU against the float64 oracle.
 
-Tolerance (written in tests/gpu_cases.py): bf16/fp16 output within max-abs 2e-2 and
-mean-abs 2e-3 of the oracle evaluated on the same rounded inputs.
+Tolerance (written in tests/gpu_cases.py): bf16 output within max-abs 2e-2 and mean-abs
+2e-3 of the oracle evaluated on the same rounded inputs; fp16 output within 4e-3 / 3e-4.
 """
 
 from __future__ import annotations
@@ -262,27 +262,97 @@ def test_validation_errors(device):
                         block_table=tick.block_table.long())
 
 
-@pytest.mark.parametrize("name", ["c1", "mixed"])
+@pytest.mark.parametrize("name", ["c1", "mixed", "c2", "c3"])
 def test_fused_append_matches_separate_calls(device, name):
+    """The fused append + attention call (decode rows appended inside the decode kernel,
+    chunk rows by the append kernel first) leaves the pools with the bits of a separate
+    index_copy_-style append and returns the bits of attention on the appended pool, at
+    the sizes the benchmark times (C2: 64 decode rows; C3: 32 decode rows + 2016 chunk
+    rows); the fused output is also checked against the oracle (C3: every decode row and
+    192 chunk rows)."""
     say("fused append", name)
-    w = synth.c1() if name == "c1" else synth.small_mixed(80, batch=7, max_cached=1500, max_chunk=300,
-                                                           num_pages=64)
+    big = name in ("c2", "c3")
+    w = {"c1": synth.c1, "c2": synth.c2, "c3": synth.c3}.get(name, lambda: synth.small_mixed(
+        80, batch=7, max_cached=1500, max_chunk=300, num_pages=64))()
     dtype = torch.bfloat16
-    ref = DeviceTick(w, dtype, device)          # pools already hold the appended rows
+    ref = DeviceTick(w, dtype, device, pool_on_device=big)   # pools hold the appended rows
     out_ref = ref.attend(exact_grid=True)
-    # the same inputs before the append
-    s = w.seed * 7919
-    shape = (w.num_pages, w.page_size, w.n_kv_heads, w.head_dim)
-    k_pool = torch.from_numpy(synth.normal(s + 4, shape)).to(dtype).to(device)
-    v_pool = torch.from_numpy(synth.normal(s + 5, shape)).to(dtype).to(device)
-    plan = ops.VarlenAttnPlan(
-        ref.cu_seq_q, ref.cu_seq_k, ref.seqused_k, total_q=w.total_q, max_q=w.max_q, max_k=w.max_k,
-        n_q_heads=w.n_q_heads, n_kv_heads=w.n_kv_heads, head_dim=w.head_dim, page_size=w.page_size,
-        block_table_stride=ref.block_table.shape[1], q_lens=w.q_lens, k_lens=w.k_lens)
+    k_pool, v_pool = ref.fresh_pools()                       # the same pools before the append
+    plan = ref.plan()
     out = plan.run(ref.q, k_pool, v_pool, ref.block_table,
                    append=(ref.k_new, ref.v_new, ref.write_slots))
     torch.cuda.synchronize()
     assert plan.error_word() == 0
     assert torch.equal(k_pool.view(torch.int16), ref.k_pool.view(torch.int16))
     assert torch.equal(v_pool.view(torch.int16), ref.v_pool.view(torch.int16))
-    assert torch.equal(out, out_ref)
+    assert torch.equal(out.view(torch.int16), out_ref.view(torch.int16))
+    if big:
+        decoders = [b for b, n in enumerate(w.q_lens) if n == 1]
+        rows = {b: [0] for b in decoders}
+        for b, n in enumerate(w.q_lens):
+            if n > 1:
+                sample = list(range(0, 32)) + list(range(n // 2 - 32, n // 2 + 32)) + list(range(n - 32, n))
+                rows[b] = sample
+        ref_out, _ = ref.oracle(rows=rows)
+        flat = [w.cu_seq_q[b] + r for b, rs in rows.items() for r in rs]
+        compare(out, ref_out, what=f"fused {name}", rows=np.array(sorted(flat)))
+
+
+@pytest.mark.parametrize("sharp", [1.0, 6.0])
+def test_fp16_split_partials_keep_fp16_precision(device, sharp):
+    """fp16 end to end with split partials on both paths: decode rows of 700-4000 keys
+    (up to 16 splits, merged by the combine kernel) and two short chunks whose row blocks
+    the plan splits over key tiles. Queries scaled by ``sharp`` make the softmax
+    concentrate, so outputs are close to single V rows and any partial rounded to fewer
+    than fp16's bits would exceed the fp16 bound (tests/gpu_cases.py: 4e-3 / 3e-4)."""
+    say("fp16 split partials", sharp)
+    q_lens = [1] * 12 + [200, 130]
+    k_lens = [700, 1300, 2100, 4000, 3333, 257, 1024, 3999, 1800, 2600, 900, 3100, 1500, 1100]
+    pages = sum(-(-L // 256) for L in k_lens)
+    perm = [int(p) for p in np.random.default_rng(21).permutation(pages + 4)]
+    tables, i = [], 0
+    for L in k_lens:
+        tables.append(perm[i:i + -(-L // 256)])
+        i += -(-L // 256)
+    w = synth.Workload("fp16 splits", q_lens, [L - n for n, L in zip(q_lens, k_lens)], tables, pages + 4,
+                       seed=21)
+    n_dec, n_pf, n_comb = ops.count_items(q_lens, k_lens, 32, 8, (-1, 0))
+    long_decoders = sum(1 for n, L in zip(q_lens, k_lens) if n == 1 and L > 256)
+    assert n_comb > long_decoders, "the chunk row blocks should be split over key tiles"
+    tick = DeviceTick(w, torch.float16, device)
+    tick.q.mul_(sharp)
+    ref, _ = tick.oracle()
+    out = tick.attend(exact_grid=True)
+    assert out.dtype == torch.float16
+    compare(out, ref, what=f"fp16 splits x{sharp}")
+
+
+def test_fused_append_ignores_stale_pool_rows(device):
+    """A decode row whose new token is the only visible key of its 256-key split
+    (L = 256k + 1) has every other row of that split masked. Before the fused call writes
+    the token, its pool slot and the rest of the page hold stale data; here that is NaN
+    and Inf bit patterns (as uninitialised or reused pool memory may hold). The output
+    must equal, bit for bit, attention over a pool whose slots held finite data."""
+    say("fused append over stale rows")
+    cached = [256, 512, 4096, 1000, 767, 1024]
+    q_lens = [1] * len(cached)
+    pages = sum(-(-(n + 1) // 256) for n in cached)
+    perm = [int(p) for p in np.random.default_rng(31).permutation(pages + 2)]
+    tables, i = [], 0
+    for n in cached:
+        tables.append(perm[i:i + -(-(n + 1) // 256)])
+        i += -(-(n + 1) // 256)
+    w = synth.Workload("stale rows", q_lens, cached, tables, pages + 2, seed=31)
+    tick = DeviceTick(w, torch.bfloat16, device)      # finite pools, tokens appended
+    want = tick.attend(exact_grid=True)
+    k_pool, v_pool = tick.fresh_pools()
+    for b, n in enumerate(cached):                    # stale data from the new slot to page end
+        page, off = tables[b][n // 256], n % 256
+        k_pool[page, off:].view(torch.int16).fill_(0x7FC0)   # NaN
+        v_pool[page, off:].view(torch.int16).fill_(0x7F80)   # +Inf
+    plan = tick.plan()
+    out = plan.run(tick.q, k_pool, v_pool, tick.block_table,
+                   append=(tick.k_new, tick.v_new, tick.write_slots))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))

@@ -11,7 +11,7 @@ from helios_amd import ops
 from helios_amd.config import Qwen3Config
 from helios_amd.paged_cache import KVPagePool, PackedBatchCache, PagedBatchCache, PagedKVCache, _PrefixCascade
 from oracle import attention
-from tests.gpu_cases import MAX_ABS, MEAN_ABS, say
+from tests.gpu_cases import say, tolerance
 
 pytestmark = pytest.mark.gpu
 
@@ -53,9 +53,11 @@ def _oracle(pool, caches, counts, q, layer=0):
     return out
 
 
-def _compare(got, want, what):
+def _compare(got, want, what, dtype=torch.bfloat16):
+    max_abs, mean_abs = tolerance(dtype)
     err = np.abs(got - want)
-    assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (what, err.max(), err.mean())
+    say(what, f"max_abs={err.max():.3e} mean_abs={err.mean():.3e}")
+    assert err.max() <= max_abs and err.mean() <= mean_abs, (what, err.max(), err.mean())
 
 
 @pytest.fixture
@@ -105,10 +107,10 @@ def test_cascade_matches_oracle_and_plain_path(device, counts_kind, dtype, alway
         torch.cuda.synchronize()
         want = _oracle(pool, caches, counts, q[0].transpose(0, 1))
         got = out[0].transpose(0, 1).float().cpu().numpy()
-        _compare(got, want, f"cascade={cascade}")
+        _compare(got, want, f"cascade={cascade} {dtype}", dtype)
         outs.append(got)
         batch.advance_packed()
-    _compare(outs[0], outs[1], "cascade vs plain")
+    _compare(outs[0], outs[1], "cascade vs plain", dtype)
 
 
 @pytest.mark.parametrize("n_heads,n_kv_heads", [(64, 8), (16, 8)])

@@ -164,3 +164,35 @@ def test_gather_narrow_rows_take_the_generic_path(device, dtype, heads, dim):
     torch.cuda.synchronize()
     ref = pool.index_select(0, torch.tensor([2, 0, 3], device=device)).reshape(-1, heads, dim)[:700]
     assert torch.equal(got[0].permute(1, 0, 2), ref)
+
+
+def test_c4_restore_of_16_prefix_pages_over_36_layers(device):
+    """The C4 restore at its full size, through the pool: a request restores a 16-page
+    prefix snapshot with ``restore_blocks(copy=True)``, which copies those pages for all
+    36 layers, K and V (72 tensors of [pages, 256, 8, 128] bf16, more than one launch
+    takes). Every destination page equals its source bit for bit, as torch's copy_ of
+    the same pages gives, and no other page changes."""
+    from helios_amd.config import Qwen3Config
+    from helios_amd.paged_cache import KVPagePool, PagedKVCache
+
+    say("c4 restore 36 layers x 16 pages")
+    config = Qwen3Config()
+    pool = KVPagePool(config, 40, device=device)
+    g = torch.Generator(device=device).manual_seed(17)
+    flat = pool.storage.view(torch.int16)
+    flat.copy_(torch.randint(-32768, 32767, flat.shape, generator=g, device=device, dtype=torch.int16))
+    source = PagedKVCache(pool, config.context_length)
+    source.pages.extend(pool.acquire(18))
+    source.length = 16 * 256 + 300
+    snapshot = source.snapshot_block(0, 16 * 256)
+    before = flat.clone()
+    request = PagedKVCache(pool, config.context_length)
+    request.restore_blocks([snapshot], copy=True)
+    torch.cuda.synchronize()
+    src = [p.index for p in snapshot.pages]
+    dst = [p.index for p in request.pages]
+    assert len(dst) == 16 and not set(src) & set(dst) and request.length == 16 * 256
+    expect = before.clone()
+    expect[:, :, dst] = before[:, :, src]      # torch's copy of the same pages, every layer
+    assert torch.equal(flat, expect)
+    assert all(p not in src for p in dst) and request.pages[0] is not snapshot.pages[0]

@@ -252,3 +252,79 @@ def test_validate_attention_inputs_errors(pool):
         _validate_attention_inputs(batch, 0, torch.randn(1, 3, 3, 8), k, k)
     with pytest.raises(ValueError):
         _validate_attention_inputs(batch, 0, q, k, torch.randn(1, 1, 2, 8))
+
+
+def test_pool_is_one_allocation_of_contiguous_layer_views():
+    cfg = tiny_config()
+    p = KVPagePool(cfg, 3, device="cpu")
+    base = p.storage.data_ptr()
+    layer_bytes = 3 * 256 * 1 * 8 * 4
+    for layer in range(cfg.n_layers):
+        assert p.keys[layer].is_contiguous() and p.values[layer].is_contiguous()
+        assert p.keys[layer].data_ptr() == base + layer * layer_bytes
+        assert p.values[layer].data_ptr() == base + (cfg.n_layers + layer) * layer_bytes
+    p.keys[1][2].fill_(5.0)
+    assert bool((p.storage[0, 1, 2] == 5.0).all())
+
+
+def test_released_ids_come_back_last_in_first_out(pool):
+    a, b, c = pool.acquire(3)
+    assert [a.index, b.index, c.index] == [0, 1, 2]
+    del b
+    del a
+    # 0 was released last, so it comes back first; then 1; then the untouched 3, 4, 5
+    assert [p.index for p in pool.acquire(4)] == [0, 1, 3, 4]
+
+
+def test_metadata_reuses_the_tensor_and_uploads_on_change(pool):
+    batch = PagedBatchCache([PagedKVCache(pool, 512)])
+    t = batch.metadata("token_ids", [5, 6, 7], torch.long)
+    assert t.dtype == torch.int64 and t.tolist() == [5, 6, 7]
+    assert batch.metadata("token_ids", [5, 6, 7], torch.long) is t
+    assert batch.metadata("token_ids", [5, 6, 8], torch.long) is t and t.tolist() == [5, 6, 8]
+    u = batch.metadata("token_ids", [1, 2], torch.long)
+    assert u.tolist() == [1, 2]
+    grid = batch.metadata("grid", [[1, 2, 3], [4, 5, 6]], torch.int32)
+    assert grid.shape == (2, 3) and grid.dtype == torch.int32 and grid.tolist() == [[1, 2, 3], [4, 5, 6]]
+
+
+def test_batch_object_reused_with_other_caches(pool):
+    # The reference's decoder keeps one batch object and reassigns caches / batch_size
+    # every tick (decode.py:235-241, :278-281).
+    caches = [PagedKVCache(pool, 512) for _ in range(3)]
+    batch = PagedBatchCache(caches[:1])
+    for rows in (caches[:1], caches, caches[1:], caches):
+        batch.caches, batch.batch_size = tuple(rows), len(rows)
+        batch.prepare(1)
+        lengths = [c.length for c in rows]
+        assert batch.seqused_k.tolist() == [n + 1 for n in lengths]
+        assert batch.cu_seq_q.tolist() == list(range(len(rows) + 1))
+        assert batch.write_slots.tolist() == [c.pages[0].index * 256 + n for c, n in zip(rows, lengths)]
+        assert batch.block_table.shape == (len(rows), 2)
+        batch.advance(1)
+    assert [c.length for c in caches] == [3, 3, 3]
+
+
+def test_packed_batch_reused_with_other_caches(pool):
+    caches = [PagedKVCache(pool, 512) for _ in range(3)]
+    batch = PackedBatchCache(caches)
+    batch.prepare_packed([2, 3, 1], logit_counts=[1, 3, 1])
+    assert batch.logit_indices.tolist() == [1, 2, 3, 4, 5]
+    batch.advance_packed()
+    batch.caches, batch.batch_size = (caches[2], caches[0]), 2
+    batch.prepare_packed([4, 1])
+    assert batch.cu_seq_q.tolist() == [0, 4, 5]
+    assert batch.seqused_k.tolist() == [5, 3]
+    assert batch.positions[0].tolist() == [1, 2, 3, 4, 2]
+    assert batch.logit_indices.tolist() == [3, 4]
+    batch.advance_packed()
+    assert [c.length for c in caches] == [3, 3, 5]
+
+
+def test_copying_restore_needs_a_device_pool(pool):
+    cache = PagedKVCache(pool, 512)
+    step([cache], 256)
+    snap = cache.snapshot_block(0, 256)
+    other = PagedKVCache(pool, 512)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        other.restore_blocks([snap], copy=True)
