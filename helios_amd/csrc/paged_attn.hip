@@ -91,8 +91,9 @@ struct Layout {
 // Partial slots: decode splits use [0, max_dec), chunk split rows [max_dec, + cslot_cap).
 // Splitting happens only while the unsplit items launch < kChunkFillWGs workgroups, and
 // the split size keeps the split items near that many, so sum over row blocks of the
-// split count is below 2 * kChunkFillWGs / (hkv * head_quads): that bounds the chunk
-// partial rows, and each split adds at most one item per block and head quad.
+// split count is below 2 * kChunkFillWGs / (hkv * head_quads); a block has at most
+// min(rows_per_item, max_q) rows, so that bounds the chunk partial rows. Each split adds
+// at most one item per block and head quad.
 inline Layout make_layout(int batch, int max_q, int max_k, int hq, int hkv) {
   const Geometry geo = geometry(hq, hkv);
   Layout l;
@@ -102,7 +103,8 @@ inline Layout make_layout(int batch, int max_q, int max_k, int hq, int hkv) {
   l.cslot_cap = 0;
   if (max_q >= 2) {
     l.max_pf = (int64_t)batch * ceil_div(max_q, geo.rows_per_item) * geo.head_quads + 2 * kChunkFillWGs;
-    l.cslot_cap = ceil_div(2 * kChunkFillWGs, (int64_t)hkv * geo.head_quads) * geo.rows_per_item;
+    const int64_t block_rows = max_q < geo.rows_per_item ? max_q : geo.rows_per_item;
+    l.cslot_cap = ceil_div(2 * kChunkFillWGs, (int64_t)hkv * geo.head_quads) * block_rows;
   }
   l.max_comb = (int64_t)batch + l.cslot_cap;
   size_t off = align256(H_WORDS * sizeof(int32_t));
