@@ -13,11 +13,12 @@ HEADER_PATH = Path(__file__).resolve().parent.parent / "include" / "helios_paged
 
 HX_OK = 0
 # hx_abi_version() of the library these signatures describe (bumped on any signature change).
-ABI_VERSION = 2
+ABI_VERSION = 3
 HX_E_INVALID_ARG = -1
 HX_E_UNSUPPORTED = -2
 HX_E_WORKSPACE = -3
 HX_E_OVERLAP = -4
+HX_E_TOO_LARGE = -5
 
 HX_DTYPE_BF16 = 0
 HX_DTYPE_FP16 = 1
@@ -110,6 +111,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_void_p, _size, _c_void_p],
     ),
     "hx_varlen_attn_error_word_offset": (_size, []),
+    "hx_varlen_attn_noalloc": (
+        ctypes.c_int,
+        [_c_void_p, _i64, _i64,
+         _c_void_p, _c_void_p, _i64, _i64,
+         _i32, _i32, _c_void_p, _i32,
+         _c_void_p, _c_void_p, _c_void_p,
+         _i32, _i32, _i32, _i32, _i64,
+         _i32, _i32, _i32,
+         _f32, _i32, _i32, _i32,
+         _c_void_p, _i64, _i64, _c_void_p,
+         _c_void_p],
+    ),
     "hx_qk_norm_rope_append": (
         ctypes.c_int,
         [_c_void_p, _i64, _i64,

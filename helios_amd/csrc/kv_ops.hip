@@ -195,13 +195,14 @@ const char* hx_strerror(int code) {
     case HX_E_UNSUPPORTED: return "unsupported head_dim, group size or dtype";
     case HX_E_WORKSPACE: return "workspace missing, misaligned or too small";
     case HX_E_OVERLAP: return "page copy sources and destinations overlap";
+    case HX_E_TOO_LARGE: return "the call needs more workspace than the no-allocation scratch holds";
     default: break;
   }
   if (code > 0) return hipGetErrorString((hipError_t)code);
   return "unknown helios_paged status";
 }
 
-int hx_abi_version(void) { return 2; }
+int hx_abi_version(void) { return 3; }
 
 int hx_kv_append(void* k_pool, void* v_pool, int64_t pool_rows,
                  const void* k_new, int64_t k_row_stride, int64_t k_head_stride,

@@ -33,6 +33,8 @@
 
 #include <math.h>
 
+#include <mutex>
+
 namespace {
 
 constexpr int kD = 128;          // head_dim built
@@ -1662,6 +1664,76 @@ int hx_varlen_attn(const void* q, int64_t q_row_stride, int64_t q_head_stride,
                             batch, total_q, max_q, max_k, n_q_heads, n_kv_heads, head_dim, scale,
                             window_left, window_right, dtype, out, o_row_stride, o_head_stride, lse,
                             -1, -1, -1, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ no-allocation entry
+// Workspace of hx_varlen_attn_noalloc: one array per GPU in the library's device memory,
+// allocated with the code object when the library loads on that GPU and held until the
+// process ends. Host code never passes `scratch` itself to a kernel (on the host it is
+// only a stand-in for the symbol): it uses the device address hipGetSymbolAddress gives
+// for the current GPU, looked up once per GPU and kept in g_scratch_ptr.
+static constexpr size_t kNoallocScratchBytes = HX_NOALLOC_SCRATCH_BYTES;  // 128 MiB
+static __device__ __align__(256) uint8_t scratch[kNoallocScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of the current GPU's scratch array (resolved at this GPU's first call).
+int current_device_scratch(void** ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hx::status_from_hip(e);
+  if (dev < 0 || dev >= kMaxScratchDevices) return HX_E_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hx::status_from_hip(e);
+    if (p == nullptr || reinterpret_cast<uintptr_t>(p) % 256 != 0) return HX_E_WORKSPACE;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return HX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hx_varlen_attn_noalloc(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                           const void* k_cache, const void* v_cache,
+                           int64_t kv_row_stride, int64_t kv_head_stride,
+                           int32_t num_pages, int32_t page_size,
+                           const int32_t* block_table, int32_t block_table_stride,
+                           const int32_t* cu_seq_q, const int32_t* cu_seq_k,
+                           const int32_t* seqused_k,
+                           int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                           int64_t total_k_rows,
+                           int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                           float scale, int32_t window_left, int32_t window_right,
+                           int32_t dtype,
+                           void* out, int64_t o_row_stride, int64_t o_head_stride,
+                           float* lse, void* stream) {
+  const int st = check_shape(batch, max_q, max_k, n_q_heads, n_kv_heads, head_dim);
+  if (st != HX_OK) return st;
+  // The plan and the split partials of this call must fit the scratch array.
+  if (make_layout(batch, max_q, max_k, n_q_heads, n_kv_heads).total > kNoallocScratchBytes)
+    return HX_E_TOO_LARGE;
+  void* ws = nullptr;
+  const int sst = current_device_scratch(&ws);
+  if (sst != HX_OK) return sst;
+  // Every word the run kernels read is written by the plan kernel of this call first
+  // (stream order), so nothing left in the array by an earlier call needs clearing.
+  return hx_varlen_attn(q, q_row_stride, q_head_stride, k_cache, v_cache, kv_row_stride,
+                        kv_head_stride, num_pages, page_size, block_table, block_table_stride,
+                        cu_seq_q, cu_seq_k, seqused_k, batch, total_q, max_q, max_k, total_k_rows,
+                        n_q_heads, n_kv_heads, head_dim, scale, window_left, window_right, dtype,
+                        out, o_row_stride, o_head_stride, lse, ws, kNoallocScratchBytes, stream);
 }
 
 }  // extern "C"

@@ -43,6 +43,7 @@ extern "C" {
 #define HX_E_UNSUPPORTED (-2)   /* head_dim / group size / dtype not built         */
 #define HX_E_WORKSPACE (-3)     /* workspace missing, misaligned or too small      */
 #define HX_E_OVERLAP (-4)       /* page copy source and destination sets overlap   */
+#define HX_E_TOO_LARGE (-5)     /* beyond the no-allocation scratch (hx_varlen_attn_noalloc) */
 
 /* ---- element types -------------------------------------------------------- */
 #define HX_DTYPE_BF16 0
@@ -229,6 +230,42 @@ int hx_varlen_attn(const void* q, int64_t q_row_stride, int64_t q_head_stride,
 /* Byte offset of the int32 error word inside the workspace (OR of HX_WERR_* bits,
  * cleared by each hx_varlen_attn_plan). */
 size_t hx_varlen_attn_error_word_offset(void);
+
+/*
+ * hx_varlen_attn without a workspace argument, for callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc. No counterpart in the reference (whose varlen_attn allocates through
+ * torch). Same arguments and results as hx_varlen_attn; the plan and the split partials
+ * live in a device array of HX_NOALLOC_SCRATCH_BYTES that the library holds on every
+ * GPU it runs on until the process ends. The call allocates nothing: the array's device
+ * address is looked up once per GPU, at that GPU's first call (make that first call
+ * outside graph capture), with the stream's GPU current.
+ *   - A shape whose workspace (hx_varlen_attn_workspace_bytes) exceeds the array
+ *     returns HX_E_TOO_LARGE before any launch. Decode ticks of up to ~15000 256-key
+ *     splits fit, and so do the mixed and long-context ticks of the Qwen3-4B
+ *     workloads (about 71-100 MiB).
+ *   - Every call on a GPU uses that GPU's one array: calls that overlap on one GPU
+ *     (different streams, or host threads without stream order between them) race.
+ *     Calls in order on one stream are safe; each call's plan rewrites what its run reads.
+ *   - The error word is not readable through this entry point (use hx_varlen_attn with
+ *     a workspace to diagnose metadata).
+ */
+#define HX_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+
+int hx_varlen_attn_noalloc(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                           const void* k_cache, const void* v_cache,
+                           int64_t kv_row_stride, int64_t kv_head_stride,
+                           int32_t num_pages, int32_t page_size,
+                           const int32_t* block_table, int32_t block_table_stride,
+                           const int32_t* cu_seq_q, const int32_t* cu_seq_k,
+                           const int32_t* seqused_k,
+                           int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                           int64_t total_k_rows,
+                           int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                           float scale, int32_t window_left, int32_t window_right,
+                           int32_t dtype,
+                           void* out, int64_t o_row_stride, int64_t o_head_stride,
+                           float* lse, void* stream);
 
 /*
  * Tick metadata on the device. Replaces the per-token list building of

@@ -33,7 +33,7 @@ def test_loader_rejects_a_library_of_another_abi_version(monkeypatch):
 
 
 def test_abi_version_and_strerror():
-    assert _capi.lib().hx_abi_version() == _capi.ABI_VERSION == 2
+    assert _capi.lib().hx_abi_version() == _capi.ABI_VERSION == 3
     assert _capi.strerror(0) == "success"
     assert "invalid" in _capi.strerror(_capi.HX_E_INVALID_ARG)
     with pytest.raises(ValueError):
@@ -164,3 +164,19 @@ def test_attention_entry_points_reject_bad_arguments_on_the_host():
     assert lib.hx_kv_append(16, 16, 10, 16, 8, 8, 16, 8, 8, 16, 1, 1, 8, 3, None) == _capi.HX_E_INVALID_ARG
     # gather: length beyond the listed pages
     assert lib.hx_kv_gather(16, 4, 256, 8, 128, 2, 16, 1, 257, 16, None) == _capi.HX_E_INVALID_ARG
+
+
+def test_noalloc_rejects_a_tick_beyond_its_scratch():
+    """hx_varlen_attn_noalloc checks the shape against its scratch array before it touches
+    the device: a tick whose workspace exceeds HX_NOALLOC_SCRATCH_BYTES (128 MiB) returns
+    HX_E_TOO_LARGE, and an unsupported head_dim HX_E_UNSUPPORTED, with no launch."""
+    lib = _capi.lib()
+    batch, max_k = 4096, 32768
+    assert lib.hx_varlen_attn_workspace_bytes(batch, 1, max_k, 32, 8, 128) > 128 << 20
+    args = [None, 0, 0, None, None, 0, 0, 1, 256, None, 128, None, None, None,
+            batch, batch, 1, max_k, 0, 32, 8, 128, 1 / math.sqrt(128), -1, 0, _capi.HX_DTYPE_BF16,
+            None, 0, 0, None, None]
+    assert lib.hx_varlen_attn_noalloc(*args) == _capi.HX_E_TOO_LARGE
+    args[21] = 96   # head_dim
+    assert lib.hx_varlen_attn_noalloc(*args) == _capi.HX_E_UNSUPPORTED
+    assert "no-allocation scratch" in _capi.strerror(_capi.HX_E_TOO_LARGE)
