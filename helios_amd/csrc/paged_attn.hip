@@ -1290,6 +1290,181 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   }
 }
 
+// ------------------------------------------------------------------ any head_dim
+// Attention for shapes the tuned kernels do not cover: head_dim any multiple of 8 up to
+// 256, and any group size G. One workgroup per (sequence, block of query rows, KV head
+// g, block of up to kGenUnits of g's query heads); its (row, head) units share every K/V
+// tile read. Keys go through LDS kGenTile at a time. Lane j scores key j of the tile for
+// each of its wave's units, the softmax runs online per unit in fp32, and lane j
+// accumulates O for dims j, j + 64, ... of every unit, reading each key's p from LDS.
+// Decode and chunk rows alike, with no split-K: head_dim 128 with G in {1, 2, 4, 8}
+// goes to the decode / chunk kernels instead.
+constexpr int kGenUnits = 16;    // (row, head) units per workgroup, 4 per wave
+constexpr int kGenTile = 64;     // keys per LDS tile: one per lane
+
+struct GenericShape {
+  int32_t head_dim, group, heads_per_item, rows_per_item, row_blocks, head_blocks;
+};
+
+inline GenericShape generic_shape(int max_q, int G, int head_dim) {
+  GenericShape g;
+  g.head_dim = head_dim;
+  g.group = G;
+  g.heads_per_item = G < kGenUnits ? G : kGenUnits;
+  g.rows_per_item = kGenUnits / g.heads_per_item;
+  g.row_blocks = (int)ceil_div(max_q > 0 ? max_q : 1, g.rows_per_item);
+  g.head_blocks = (int)ceil_div(G, g.heads_per_item);
+  return g;
+}
+
+template <typename T, int DMAX>
+__global__ __launch_bounds__(256) void generic_kernel(RunArgs a, GenericShape gs) {
+  typedef hx::Elem<T> E;
+  constexpr int KS = DMAX + 8;                      // K tile row stride (elements)
+  constexpr int NC = DMAX >= 64 ? DMAX / 64 : 1;    // O dims per lane and unit
+  __shared__ __attribute__((aligned(16))) T k_lds[kGenTile * KS];
+  __shared__ __attribute__((aligned(16))) T v_lds[kGenTile * DMAX];
+  __shared__ __attribute__((aligned(16))) float q_lds[kGenUnits * DMAX];
+  __shared__ float p_lds[kGenUnits][kGenTile];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int D = gs.head_dim;
+  int x = (int)blockIdx.x;
+  const int hb = x % gs.head_blocks;
+  x /= gs.head_blocks;
+  const int g = x % a.hkv;
+  x /= a.hkv;
+  const int rb = x % gs.row_blocks;
+  const int b = x / gs.row_blocks;
+  const Header hd = read_header(a);
+  if (!hd.ok || b >= a.batch) return;
+  const int4 si = a.seq_info[b];
+  const int q0 = si.x, n = si.y, L = si.z, kvb = si.w;
+  const int row0 = rb * gs.rows_per_item;
+  if (row0 >= n) return;
+  const int rows = min(gs.rows_per_item, n - row0);
+  const int h0 = hb * gs.heads_per_item;
+  const int hcount = min(gs.heads_per_item, gs.group - h0);
+  const int units = rows * hcount;  // unit u: row row0 + u / hcount, head g*G + h0 + u % hcount
+
+  // The units' queries, widened to fp32.
+  for (int idx = tid; idx < units * D; idx += 256) {
+    const int u = idx / D, d = idx - (idx / D) * D;
+    const int64_t qrow = q0 + row0 + u / hcount;
+    const int qh = g * gs.group + h0 + u % hcount;
+    q_lds[u * DMAX + d] = E::lo(reinterpret_cast<const uint16_t*>(a.q)[qrow * a.q_row + (int64_t)qh * a.q_head + d]);
+  }
+  // Keys any row of the block can see: [klo, khi].
+  const int qfirst = L - n + row0, qlast = L - n + row0 + rows - 1;
+  const int klo = a.win_left >= 0 ? max(0, qfirst - a.win_left) : 0;
+  int khi = L - 1;
+  if (a.win_right >= 0) khi = min(khi, qlast + a.win_right);
+
+  float m[4], l[4], o[4][NC];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    m[k] = -INFINITY;
+    l[k] = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) o[k][c] = 0.f;
+  }
+  const int chunks = D / 8;  // 16-byte pieces of a head row
+  const T* kbase = reinterpret_cast<const T*>(a.k) + (int64_t)g * a.kv_head;
+  const T* vbase = reinterpret_cast<const T*>(a.v) + (int64_t)g * a.kv_head;
+  for (int t0 = khi >= klo ? (klo / kGenTile) * kGenTile : 0; khi >= klo && t0 <= khi; t0 += kGenTile) {
+    __syncthreads();  // the previous tile's readers are done
+    // K and V rows of keys t0 .. t0 + 63; keys past L - 1 re-read row L - 1 (masked).
+    for (int idx = tid; idx < kGenTile * chunks; idx += 256) {
+      const int key = idx / chunks, c8 = idx - (idx / chunks) * chunks;
+      const int kk = min(t0 + key, L - 1);
+      int64_t row;
+      if (a.page_size > 0) {
+        int page = a.bt[(int64_t)b * a.bt_stride + kk / a.page_size];
+        if ((unsigned)page >= (unsigned)a.num_pages) {
+          atomicOr(&a.hdr[H_ERR], HX_WERR_BAD_PAGE);
+          page = 0;
+        }
+        row = (int64_t)page * a.page_size + kk % a.page_size;
+      } else {
+        row = (int64_t)kvb + kk;
+      }
+      *reinterpret_cast<uint4*>(&k_lds[key * KS + 8 * c8]) = ld16(kbase + row * a.kv_row + 8 * c8);
+      *reinterpret_cast<uint4*>(&v_lds[key * DMAX + 8 * c8]) = ld16(vbase + row * a.kv_row + 8 * c8);
+    }
+    __syncthreads();
+    // Scores and online softmax: lane j holds key t0 + j of each of the wave's units.
+    const int kk = t0 + lane;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int c8 = 0; c8 < chunks; ++c8) {
+      const uint4 kv = *reinterpret_cast<const uint4*>(&k_lds[lane * KS + 8 * c8]);
+      const float kf[8] = {E::lo(kv.x), E::hi(kv.x), E::lo(kv.y), E::hi(kv.y),
+                           E::lo(kv.z), E::hi(kv.z), E::lo(kv.w), E::hi(kv.w)};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int u = w + 4 * k;
+        if (u < units) {
+          const float4 qa = *reinterpret_cast<const float4*>(&q_lds[u * DMAX + 8 * c8]);
+          const float4 qb = *reinterpret_cast<const float4*>(&q_lds[u * DMAX + 8 * c8 + 4]);
+          s[k] += qa.x * kf[0] + qa.y * kf[1] + qa.z * kf[2] + qa.w * kf[3] +
+                  qb.x * kf[4] + qb.y * kf[5] + qb.z * kf[6] + qb.w * kf[7];
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int u = w + 4 * k;
+      if (u >= units) continue;  // wave-uniform
+      const int qpos = L - n + row0 + u / hcount;
+      const bool vis = kk <= L - 1 && (a.win_left < 0 || kk >= qpos - a.win_left) &&
+                       (a.win_right < 0 || kk <= qpos + a.win_right);
+      const float sc = vis ? s[k] * a.scale_log2 : -INFINITY;
+      const float m_new = fmaxf(m[k], wave_max(sc));
+      float p = 0.f, alpha = 1.f;
+      if (m_new != -INFINITY) {
+        p = vis ? hx::fast_exp2(sc - m_new) : 0.f;
+        alpha = m[k] == -INFINITY ? 0.f : hx::fast_exp2(m[k] - m_new);
+      }
+      l[k] = l[k] * alpha + wave_sum(p);
+      m[k] = m_new;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) o[k][c] *= alpha;
+      p_lds[u][lane] = p;
+    }
+    __syncthreads();
+    // O += P V: lane owns dims lane + 64c.
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int u = w + 4 * k;
+      if (u >= units) continue;
+      for (int j = 0; j < kGenTile; ++j) {
+        const float pj = p_lds[u][j];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int d = lane + 64 * c;
+          if (d < D) o[k][c] = fmaf(pj, E::lo(reinterpret_cast<const uint16_t*>(v_lds)[j * DMAX + d]), o[k][c]);
+        }
+      }
+    }
+  }
+  // Normalise and store every unit of this wave.
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int u = w + 4 * k;
+    if (u >= units) continue;
+    const int64_t orow = q0 + row0 + u / hcount;
+    const int qh = g * gs.group + h0 + u % hcount;
+    const float inv = l[k] > 0.f ? 1.f / l[k] : 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = lane + 64 * c;
+      if (d < D)
+        reinterpret_cast<uint16_t*>(a.out)[orow * a.o_row + (int64_t)qh * a.o_head + d] = E::bits(o[k][c] * inv);
+    }
+    if (a.lse && lane == 0)
+      a.lse[(int64_t)qh * a.total_q + orow] = l[k] > 0.f ? (m[k] + log2f(l[k])) * kLn2 : -INFINITY;
+  }
+}
+
 // ------------------------------------------------------------------ host helpers
 bool valid_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
 
@@ -1319,11 +1494,32 @@ int launch_run_g(const RunArgs& a, int G, hipStream_t s) {
   }
 }
 
+// head_dim 128 with G in {1, 2, 4, 8} runs the decode / chunk / combine kernels; every
+// other supported shape runs generic_kernel.
+bool tuned_shape(int G, int head_dim) { return head_dim == kD && valid_group(G); }
+
 int check_shape(int batch, int max_q, int max_k, int hq, int hkv, int head_dim) {
   if (batch < 0 || max_q < 0 || max_k < 0 || hq < 1 || hkv < 1) return HX_E_INVALID_ARG;
   if (hq % hkv) return HX_E_INVALID_ARG;
-  if (!valid_group(hq / hkv) || head_dim != kD) return HX_E_UNSUPPORTED;
+  if (head_dim < 8 || head_dim > 256 || head_dim % 8) return HX_E_UNSUPPORTED;
   return HX_OK;
+}
+
+template <typename T>
+int launch_generic(const RunArgs& a, const GenericShape& gs, hipStream_t s) {
+  const int64_t grid = (int64_t)a.batch * gs.row_blocks * a.hkv * gs.head_blocks;
+  if (grid > INT32_MAX) return HX_E_INVALID_ARG;
+  if (grid == 0) return HX_OK;
+  const dim3 g3((unsigned)grid), b3(256);
+  if (gs.head_dim <= 32)
+    hipLaunchKernelGGL((generic_kernel<T, 32>), g3, b3, 0, s, a, gs);
+  else if (gs.head_dim <= 64)
+    hipLaunchKernelGGL((generic_kernel<T, 64>), g3, b3, 0, s, a, gs);
+  else if (gs.head_dim <= 128)
+    hipLaunchKernelGGL((generic_kernel<T, 128>), g3, b3, 0, s, a, gs);
+  else
+    hipLaunchKernelGGL((generic_kernel<T, 256>), g3, b3, 0, s, a, gs);
+  return hx::status_from_hip(hipGetLastError());
 }
 
 }  // namespace
@@ -1548,6 +1744,8 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
   a.kn_row = a.kn_head = a.vn_row = a.vn_head = 0;
   a.pool_rows = 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int G = n_q_heads / n_kv_heads;
+  const bool tuned = tuned_shape(G, head_dim);
   if (app != nullptr && total_q > 0) {
     if (!app->k_new || !app->v_new || !app->write_slots) return HX_E_INVALID_ARG;
     // Write slots index pool rows of n_kv_heads * head_dim contiguous elements (the pool
@@ -1559,8 +1757,9 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
         app->kn_head % 8 || app->vn_row % 8 || app->vn_head % 8 || app->kn_row < 0 ||
         app->kn_head < 0 || app->vn_row < 0 || app->vn_head < 0 || app->pool_rows < 0)
       return HX_E_INVALID_ARG;
-    // Chunk rows read their own new keys from the pool: append every row first.
-    if (a.grid_pf > 0) {
+    // Chunk rows (and every row of generic_kernel) read their own new keys from the
+    // pool: append every row first.
+    if (a.grid_pf > 0 || !tuned) {
       const int elem = 2;
       const int st2 = hx_kv_append(const_cast<void*>(k_cache), const_cast<void*>(v_cache), app->pool_rows,
                                    app->k_new, app->kn_row, app->kn_head, app->v_new, app->vn_row,
@@ -1568,16 +1767,25 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
                                    stream);
       if (st2 != HX_OK) return st2;
     }
-    a.k_new = static_cast<const uint8_t*>(app->k_new);
-    a.v_new = static_cast<const uint8_t*>(app->v_new);
-    a.write_slots = app->write_slots;
-    a.kn_row = app->kn_row;
-    a.kn_head = app->kn_head;
-    a.vn_row = app->vn_row;
-    a.vn_head = app->vn_head;
-    a.pool_rows = app->pool_rows;
+    if (tuned) {
+      a.k_new = static_cast<const uint8_t*>(app->k_new);
+      a.v_new = static_cast<const uint8_t*>(app->v_new);
+      a.write_slots = app->write_slots;
+      a.kn_row = app->kn_row;
+      a.kn_head = app->kn_head;
+      a.vn_row = app->vn_row;
+      a.vn_head = app->vn_head;
+      a.pool_rows = app->pool_rows;
+    }
   }
-  const int G = n_q_heads / n_kv_heads;
+  if (!tuned) {
+    // One kernel covers every row; a call whose hints launch neither decode nor chunk
+    // work (the combine-only phase of a split run) launches nothing.
+    if (decode_items_hint == 0 && prefill_items_hint == 0) return HX_OK;
+    const GenericShape gs = generic_shape(max_q, G, head_dim);
+    if (dtype == HX_DTYPE_BF16) return launch_generic<__bf16>(a, gs, s);
+    return launch_generic<_Float16>(a, gs, s);
+  }
   if (dtype == HX_DTYPE_BF16) return launch_run_g<__bf16>(a, G, s);
   return launch_run_g<_Float16>(a, G, s);
 }

@@ -455,8 +455,8 @@ def workspace_bytes(batch: int, max_q: int, max_k: int, n_q_heads: int, n_kv_hea
     nbytes = _capi.lib().hx_varlen_attn_workspace_bytes(batch, max_q, max_k, n_q_heads, n_kv_heads, head_dim)
     if nbytes == 0:
         raise ValueError(
-            "Unsupported attention shape: head_dim must be 128 and n_q_heads / n_kv_heads "
-            "one of 1, 2, 4, 8."
+            "Unsupported attention shape: head_dim must be a multiple of 8 from 8 to 256 and "
+            "n_q_heads a multiple of n_kv_heads."
         )
     return nbytes
 

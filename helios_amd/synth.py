@@ -241,7 +241,7 @@ def c4(seed: int = 4, num_pages: int = 1024) -> Workload:
 
 def small_mixed(seed: int, *, n_q_heads: int = 32, n_kv_heads: int = 8, batch: int = 6,
                 max_cached: int = 900, max_chunk: int = 200, num_pages: int = 64,
-                page_size: int = 256) -> Workload:
+                page_size: int = 256, head_dim: int = 128) -> Workload:
     """A random mixed tick small enough for the float64 oracle in a second."""
     kinds = splitmix64(seed, 3 * batch)
     q_lens, cached = [], []
@@ -254,7 +254,7 @@ def small_mixed(seed: int, *, n_q_heads: int = 32, n_kv_heads: int = 8, batch: i
     free = list(permutation(seed + 7, num_pages))
     tables = _assign_pages([c + n for c, n in zip(cached, q_lens)], free, page_size)
     return Workload(f"mixed{seed}", q_lens, cached, tables, num_pages, page_size=page_size,
-                    n_q_heads=n_q_heads, n_kv_heads=n_kv_heads, seed=seed)
+                    n_q_heads=n_q_heads, n_kv_heads=n_kv_heads, head_dim=head_dim, seed=seed)
 
 
 def host_inputs(w: Workload, dtype=np.float32) -> dict[str, np.ndarray]:

@@ -124,12 +124,15 @@ int hx_kv_gather(const void* pool, int32_t num_pool_pages, int32_t page_size,
  * page_size == 0 the keys are packed: key j of b is row cu_seq_k[b] + j of a
  * [total_k_rows, n_kv_heads, head_dim] tensor (block_table ignored).
  * A row with no visible key outputs zeros (lse = -inf).
- * Built for head_dim 128, n_q_heads / n_kv_heads in {1, 2, 4, 8}, bf16 and fp16;
- * softmax and accumulation in fp32.
+ * head_dim: any multiple of 8 from 8 to 256; n_q_heads any multiple of n_kv_heads;
+ * bf16 and fp16; softmax and accumulation in fp32.
  *
- * Work split: decode rows (n_b == 1) run a split-K kernel, one workgroup per
- * (256-key split, KV head) whose 4 query heads share each K/V read, and a
- * deterministic combine; chunk rows (n_b > 1) run a bf16/fp16 MFMA kernel.
+ * Work split at head_dim 128 with n_q_heads / n_kv_heads in {1, 2, 4, 8}: decode rows
+ * (n_b == 1) run a split-K kernel, one workgroup per (256-key split, KV head) whose
+ * query heads share each K/V read, and a deterministic combine; chunk rows (n_b > 1)
+ * run a bf16/fp16 MFMA kernel. Every other shape runs one kernel for all rows: a
+ * workgroup per (sequence, block of query rows, KV head, up to 16 of its query heads)
+ * sharing each 64-key K/V tile through LDS, with fp32 scores and P.
  *
  * The workspace (size from hx_varlen_attn_workspace_bytes, 256-byte aligned) holds
  * the work plan and the split-K partials. hx_varlen_attn_plan writes the plan from

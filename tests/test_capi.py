@@ -45,11 +45,14 @@ def test_abi_version_and_strerror():
 def test_workspace_bytes_supported_shapes():
     lib = _capi.lib()
     assert lib.hx_varlen_attn_workspace_bytes(64, 1, 4097, 32, 8, 128) > 0
-    assert lib.hx_varlen_attn_workspace_bytes(64, 1, 4097, 32, 8, 64) == 0   # head_dim
-    assert lib.hx_varlen_attn_workspace_bytes(64, 1, 4097, 48, 8, 128) == 0  # G = 6
+    # any head_dim that is a multiple of 8 up to 256, any group size (the generic kernel)
+    for hq, hkv, d in ((32, 8, 64), (48, 8, 128), (2, 1, 8), (64, 1, 256), (12, 4, 96)):
+        assert lib.hx_varlen_attn_workspace_bytes(64, 1, 4097, hq, hkv, d) > 0, (hq, hkv, d)
+    for d in (0, 4, 12, 130, 264):
+        assert lib.hx_varlen_attn_workspace_bytes(64, 1, 4097, 32, 8, d) == 0, d
     assert lib.hx_varlen_attn_workspace_bytes(64, 1, 4097, 30, 8, 128) == 0  # not a multiple
     with pytest.raises(ValueError):
-        ops.workspace_bytes(1, 1, 1, 32, 8, 96)
+        ops.workspace_bytes(1, 1, 1, 32, 8, 100)
 
 
 def _expected_counts(w: synth.Workload, window=(-1, 0)):
@@ -154,8 +157,8 @@ def test_attention_entry_points_reject_bad_arguments_on_the_host():
     # workspace missing -> HX_E_WORKSPACE before any launch
     assert lib.hx_varlen_attn_plan(16, 16, 16, 1, 1, 1, 1, 0, 256, 1, 32, 8, 128, -1, 0,
                                    None, 0, None) == _capi.HX_E_WORKSPACE
-    # unsupported head_dim / group
-    assert lib.hx_varlen_attn_plan(16, 16, 16, 1, 1, 1, 1, 0, 256, 1, 32, 8, 64, -1, 0,
+    # unsupported head_dim (not a multiple of 8)
+    assert lib.hx_varlen_attn_plan(16, 16, 16, 1, 1, 1, 1, 0, 256, 1, 32, 8, 68, -1, 0,
                                    None, 0, None) == _capi.HX_E_UNSUPPORTED
     # page size not a multiple of 256
     assert lib.hx_varlen_attn_plan(16, 16, 16, 1, 1, 1, 1, 0, 128, 1, 32, 8, 128, -1, 0,
@@ -177,6 +180,6 @@ def test_noalloc_rejects_a_tick_beyond_its_scratch():
             batch, batch, 1, max_k, 0, 32, 8, 128, 1 / math.sqrt(128), -1, 0, _capi.HX_DTYPE_BF16,
             None, 0, 0, None, None]
     assert lib.hx_varlen_attn_noalloc(*args) == _capi.HX_E_TOO_LARGE
-    args[21] = 96   # head_dim
+    args[21] = 100   # head_dim
     assert lib.hx_varlen_attn_noalloc(*args) == _capi.HX_E_UNSUPPORTED
     assert "no-allocation scratch" in _capi.strerror(_capi.HX_E_TOO_LARGE)
