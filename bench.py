@@ -11,11 +11,11 @@ Printed JSON (one line):
   value     algorithmic HBM bytes per step / step time, in GB/s: every visible key's K
             and V row (8 heads x 128 x bf16, new token included), q read, o written,
             and the append's read + write of the new rows.
-  roofline  the decode-attention kernel alone (HIP events around its launch, in a second
-            pass over the same steps so that the timed loop carries no event markers;
-            the kernel also performs the tick's KV append): its algorithmic bytes
-            (K/V + q + o + the append's read and write) / its mean duration, against
-            the 8 TB/s HBM3E peak. `traffic` = HBM bytes per launch measured
+  roofline  the decode-attention kernel alone (its launches captured in a HIP graph,
+            one per pool copy, replayed `steps` times between two HIP events after the
+            timed loop; the kernel also performs the tick's KV append): its algorithmic
+            bytes (K/V + q + o + the append's read and write) / its mean duration,
+            against the 8 TB/s HBM3E peak. `traffic` = HBM bytes per launch measured
             by rocprofv3 FETCH_SIZE + WRITE_SIZE (scaled by a copy-kernel calibration)
             when profiles/decode_c2_pmc.json holds that measurement, else null.
   packed_tick  the mixed tick (32 decoders + 1024- and 992-token chunks): one layer's
@@ -134,6 +134,44 @@ class DecodeBench:
         if events is not None:
             events[3].record()
 
+    def phase(self, layer: int, name: str):
+        """One kernel of the step alone: the decode kernel (with its fused append on a
+        decode-only tick), the chunk kernel or the combine kernel."""
+        kp, vp = self.k_pools[layer], self.v_pools[layer]
+        fused = name == "decode" and self.w.max_q == 1
+        self.plan.run(self.q, kp, vp, self.block_table, out=self.out, phases=(name,),
+                      append=(self.k_new, self.v_new, self.slots) if fused else None)
+
+    def append(self, layer: int):
+        """The separate append kernel alone (what a tick with chunk rows runs first)."""
+        self.ops.kv_append(self.k_pools[layer], self.v_pools[layer], self.slots, self.k_new, self.v_new)
+
+
+def graph_time_us(calls, replays: int) -> float:
+    """Mean device time of one call of ``calls`` (each launching one kernel), measured by
+    capturing them in one HIP graph and replaying it ``replays`` times between two
+    events on the current stream."""
+    import torch
+
+    for call in calls:   # warm (first launches, allocator) outside the graph
+        call()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for call in calls:
+            call()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / (replays * len(calls))
+    del graph
+    return us
+
 
 def cpu_baseline(w, seconds_budget: float = 20.0):
     """The reference's dense-KV attention (oracle.dense_torch) on the host cores."""
@@ -185,6 +223,47 @@ def cpu_baseline(w, seconds_budget: float = 20.0):
     }
 
 
+def cpu_tick_baseline(w, *, rows_kept: dict[int, int] | None = None, seconds_budget: float = 12.0):
+    """The reference's packed CPU branch (paged_cache.py:521-546, restated op for op in
+    oracle.dense_torch) on one layer of tick ``w``, timed on the host cores. With
+    ``rows_kept`` = {sequence: n}, only the last n query rows of those sequences are
+    computed (a bounded sample of a long chunk: the rows that see the most keys)."""
+    import torch
+
+    from oracle import dense_torch
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cached, counts = list(w.cached), list(w.q_lens)
+    for b, n in (rows_kept or {}).items():
+        cached[b] += counts[b] - n
+        counts[b] = n
+    ends = [c + n for c, n in zip(cached, counts)]
+    used = sorted({p for t, e in zip(w.tables, ends) for p in t[: -(-e // w.page_size)]})
+    remap = {p: i for i, p in enumerate(used)}
+    tables = [[remap.get(p, 0) for p in t] for t in w.tables]
+    g = torch.Generator().manual_seed(6)
+    shape = (len(used), w.page_size, w.n_kv_heads, w.head_dim)
+    kp, vp = torch.randn(shape, generator=g), torch.randn(shape, generator=g)
+    q = torch.randn((1, w.n_q_heads, sum(counts), w.head_dim), generator=g)
+    times = []
+    with torch.inference_mode():
+        for rep in range(2 + 5):
+            t0 = time.perf_counter()
+            dense_torch.packed_attention(q, kp, vp, tables, cached, counts)
+            dt = time.perf_counter() - t0
+            if rep >= 1:
+                times.append(dt)
+            if sum(times) > seconds_budget and len(times) >= 2:
+                break
+    sec = statistics.median(times)
+    flops = 4 * w.n_q_heads * w.head_dim * sum(
+        sum(min(e, c + i + 1) for i in range(n)) for c, n, e in zip(cached, counts, ends))
+    return {"rows": sum(counts), "keys_visible": flops // (4 * w.n_q_heads * w.head_dim),
+            "ms_per_layer": round(sec * 1e3, 1), "rows_per_s": round(sum(counts) / sec, 1),
+            "gflops": round(flops / sec / 1e9, 2), "cores": cores, "reps": len(times)}
+
+
 def packed_tick(device, steps: int = 30, warmup: int = 5):
     """One layer of the mixed tick: append + decode/chunk attention, wall time."""
     import torch
@@ -201,23 +280,24 @@ def packed_tick(device, steps: int = 30, warmup: int = 5):
         b.step(i % 2)
     torch.cuda.synchronize()
     sec = (time.perf_counter() - t0) / steps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
-    for i in range(steps):
-        b.step(i % 2, ev[i])
-    torch.cuda.synchronize()
-    decode_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in ev)
-    chunk_ms = statistics.mean(e[2].elapsed_time(e[3]) for e in ev)
+    assert b.plan.error_word() == 0, "attention plan reported an error"
+    # per-kernel device time, each kernel's launches replayed from a HIP graph
+    us = {name: graph_time_us([lambda i=i, name=name: b.phase(i, name) for i in range(2)], steps)
+          for name in ("decode", "chunk", "combine")}
+    us["append"] = graph_time_us([lambda i=i: b.append(i) for i in range(2)], steps)
     res = {
         "workload": "c3: 32 decoders ctx U[1024,4096] + chunks 1024@0 and 992@512, bf16",
         "tokens": w.total_q,
         "us_per_layer": round(sec * 1e6, 2),
         "tick_ms_36_layers": round(sec * N_LAYERS_MODEL * 1e3, 3),
         "tokens_per_s_attention_only": round(w.total_q / (sec * N_LAYERS_MODEL), 1),
-        "decode_rows_us": round(decode_ms * 1e3, 2),
-        "decode_rows_gbs": round(w.decode_bytes() / (decode_ms * 1e-3) / 1e9, 1),
-        "chunk_rows_us": round(chunk_ms * 1e3, 2),
-        "chunk_rows_tflops": round(w.chunk_flops() / (chunk_ms * 1e-3) / 1e12, 1),
-        "chunk_mfma_frac": round(w.chunk_flops() / (chunk_ms * 1e-3) / 2.5e15, 4),
+        "kernel_us": {k: round(v, 2) for k, v in us.items()},
+        "decode_rows_us": round(us["decode"], 2),
+        "decode_rows_gbs": round(w.decode_bytes() / (us["decode"] * 1e-6) / 1e9, 1),
+        "chunk_rows_us": round(us["chunk"] + us["combine"], 2),
+        "chunk_kernel_tflops": round(w.chunk_flops() / (us["chunk"] * 1e-6) / 1e12, 1),
+        "chunk_kernel_mfma_frac": round(w.chunk_flops() / (us["chunk"] * 1e-6) / 2.5e15, 4),
+        "chunk_rows_mfma_frac": round(w.chunk_flops() / ((us["chunk"] + us["combine"]) * 1e-6) / 2.5e15, 4),
     }
     del b
     torch.cuda.empty_cache()
@@ -236,13 +316,13 @@ def long_context(device, steps: int = 10, warmup: int = 3):
     b = DecodeBench(w, device, copies=1)
     for _ in range(warmup):
         b.step(0)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
-    for i in range(steps):
-        b.step(0, ev[i])
     torch.cuda.synchronize()
-    append_us = statistics.mean(e[0].elapsed_time(e[1]) for e in ev) * 1e3
-    decode_us = statistics.mean(e[1].elapsed_time(e[2]) for e in ev) * 1e3
-    chunk_us = statistics.mean(e[2].elapsed_time(e[3]) for e in ev) * 1e3
+    assert b.plan.error_word() == 0, "attention plan reported an error"
+    append_us = graph_time_us([lambda: b.append(0)], steps)
+    decode_us = graph_time_us([lambda: b.phase(0, "decode")], steps)
+    chunk_kernel_us = graph_time_us([lambda: b.phase(0, "chunk")], steps)
+    combine_us = graph_time_us([lambda: b.phase(0, "combine")], steps)
+    chunk_us = chunk_kernel_us + combine_us
     del b
     torch.cuda.empty_cache()
     # restore copy: 16 prefix pages of every layer, keys and values
@@ -261,7 +341,9 @@ def long_context(device, steps: int = 10, warmup: int = 3):
     torch.cuda.synchronize()
     copy_us = statistics.median(a_.elapsed_time(b_) for a_, b_ in cev) * 1e3
     copy_bytes = 2 * layers * 2 * n * kl[0][0].numel() * 2
-    assert torch.equal(kl[5][dst[3]], kl[5][src[3]]) and torch.equal(vl[35][dst[0]], vl[35][src[0]])
+    # every copied page of every layer, K and V, bit for bit (72 tensors: two launches)
+    for t in kl + vl:
+        assert torch.equal(t[dst].view(torch.int16), t[src].view(torch.int16)), "restore copy differs"
     del kl, vl
     torch.cuda.empty_cache()
     # page gather (_gather_cpu's paged -> dense [1, 8, L, 128]) of one 32768-key sequence
@@ -288,8 +370,10 @@ def long_context(device, steps: int = 10, warmup: int = 3):
         "decode_rows_us": round(decode_us, 2),
         "decode_rows_gbs_unique": round(w.decode_bytes() / (decode_us * 1e-6) / 1e9, 1),
         "chunk_rows_us": round(chunk_us, 2),
-        "chunk_rows_tflops": round(w.chunk_flops() / (chunk_us * 1e-6) / 1e12, 1),
-        "chunk_mfma_frac": round(w.chunk_flops() / (chunk_us * 1e-6) / 2.5e15, 4),
+        "chunk_kernel_us": round(chunk_kernel_us, 2),
+        "chunk_kernel_tflops": round(w.chunk_flops() / (chunk_kernel_us * 1e-6) / 1e12, 1),
+        "chunk_kernel_mfma_frac": round(w.chunk_flops() / (chunk_kernel_us * 1e-6) / 2.5e15, 4),
+        "chunk_rows_mfma_frac": round(w.chunk_flops() / (chunk_us * 1e-6) / 2.5e15, 4),
         "restore_copy_us": round(copy_us, 2),
         "restore_copy_gbs_rw": round(copy_bytes / (copy_us * 1e-6) / 1e9, 1),
         "gather_32k_keys_us": round(gather_us, 2),
@@ -639,15 +723,12 @@ def main():
     elapsed = time.perf_counter() - t0
     assert b.plan.error_word() == 0, "attention plan reported an error"
     ms_per_step = elapsed * 1e3 / args.steps
-    # Kernel timing: the same K steps again with HIP events around each launch, on the
-    # stream the kernels run on (the current stream).
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
-    for i in range(args.steps):
-        b.step(i % POOL_COPIES, events[i])
-    torch.cuda.synchronize()
-    append_us = statistics.mean(e[0].elapsed_time(e[1]) for e in events) * 1e3
-    decode_us = statistics.mean(e[1].elapsed_time(e[2]) for e in events) * 1e3
-    combine_us = statistics.mean(e[2].elapsed_time(e[3]) for e in events) * 1e3
+    # Kernel timing: each kernel launched back to back from a replayed HIP graph (one
+    # launch per pool copy, the graph replayed many times) between two HIP events on the
+    # stream the launches run on, so the mean carries no host launch gaps.
+    decode_us = graph_time_us([lambda i=i: b.phase(i, "decode") for i in range(POOL_COPIES)], args.steps)
+    combine_us = graph_time_us([lambda i=i: b.phase(i, "combine") for i in range(POOL_COPIES)], args.steps)
+    append_us = graph_time_us([lambda i=i: b.append(i) for i in range(POOL_COPIES)], args.steps)
     kernel_bytes = w.decode_bytes() + w.append_bytes()  # the decode kernel appends too
     achieved = kernel_bytes / (decode_us * 1e-6) / 1e9
     traffic = None
@@ -694,7 +775,7 @@ def main():
             "algorithmic_bytes_per_launch": kernel_bytes,
         },
     }
-    del b, events
+    del b
     torch.cuda.empty_cache()
     legs = {
         "packed_tick": packed_tick,
@@ -714,6 +795,13 @@ def main():
         result[name] = legs[name](device)
     if args.only is None and not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)
+        # The same dense-KV path on the mixed tick (whole layer) and on the long-context
+        # tick (its 8 decode rows and the last 512 of its 4096 chunk rows).
+        c4 = synth.c4()
+        result["cpu_baseline_ticks"] = {
+            "c3_mixed_tick": cpu_tick_baseline(synth.c3()),
+            "c4_sample_decoders_and_last_512_chunk_rows": cpu_tick_baseline(c4, rows_kept={8: 512}),
+        }
     print(json.dumps(result), flush=True)
 
 
