@@ -287,11 +287,26 @@ __device__ SeqMeta plan_seq(const PlanArgs& a, int b, int& err) {
   return m;
 }
 
-__global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
-  __shared__ int wave_tot[kPlanThreads / 64];
-  __shared__ int err_bits;
-  if (threadIdx.x == 0) err_bits = 0;
-  __syncthreads();
+// The plan header: item counts (clamped to the lists' capacities), the error word and the
+// stamp of the shape the plan was built for.
+__device__ void write_plan_header(const PlanArgs& a, int err, int4 totals) {
+  const int base_dec = totals.x, base_pf = totals.y, base_comb = totals.z;
+  if (base_dec > a.max_dec || base_pf > a.max_pf || base_comb > a.max_comb) err |= HX_WERR_GRID;
+  a.hdr[H_NDEC] = base_dec < a.max_dec ? base_dec : (int)a.max_dec;
+  a.hdr[H_NPF] = base_pf < a.max_pf ? base_pf : (int)a.max_pf;
+  a.hdr[H_NCOMB] = base_comb < a.max_comb ? base_comb : (int)a.max_comb;
+  a.hdr[H_ERR] = err;
+  a.hdr[H_BATCH] = a.batch;
+  a.hdr[H_MAXQ] = a.max_q;
+  a.hdr[H_MAXK] = a.max_k;
+  a.hdr[H_HQ] = a.hq;
+  a.hdr[H_HKV] = a.hkv;
+  a.hdr[H_STAMP] = kPlanStamp;
+}
+
+// The planner's serial form: one thread walks each sequence's row blocks in every pass.
+// Used when the chunk sequences or their row blocks exceed the LDS lists of plan_kernel.
+__device__ void plan_serial(const PlanArgs& a, int* wave_tot, int* err_bits, int4* totals) {
   int err = 0;
 
   // Pass 1: chunk work before splitting (items and key tiles, head quads counted; the
@@ -426,22 +441,337 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
     base_comb += tot_c;
     base_slot += tot_s;
   }
+  if (err) atomicOr(err_bits, err);
+  *totals = make_int4(base_dec, base_pf, base_comb, base_slot);
+}
+
+
+// Inclusive scan (sum, or max when MAX) over the 64 lanes of a wave by DPP: row shifts by
+// 1, 2, 4 and 8 within each 16-lane row, then the row broadcasts of lane 15 (to rows 1
+// and 3) and lane 31 (to rows 2 and 3). Lanes whose DPP source lies outside the row, or
+// whose row is masked off, take the identity.
+template <bool MAX>
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  constexpr int kId = MAX ? INT32_MIN : 0;
+  auto op = [](int p, int q) { return MAX ? max(p, q) : p + q; };
+  x = op(x, __builtin_amdgcn_update_dpp(kId, x, 0x111, 0xf, 0xf, false));  // row_shr:1
+  x = op(x, __builtin_amdgcn_update_dpp(kId, x, 0x112, 0xf, 0xf, false));  // row_shr:2
+  x = op(x, __builtin_amdgcn_update_dpp(kId, x, 0x114, 0xf, 0xf, false));  // row_shr:4
+  x = op(x, __builtin_amdgcn_update_dpp(kId, x, 0x118, 0xf, 0xf, false));  // row_shr:8
+  x = op(x, __builtin_amdgcn_update_dpp(kId, x, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  x = op(x, __builtin_amdgcn_update_dpp(kId, x, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return x;
+}
+
+// Per-wave totals for block-wide scans, in two buffers used in turn: a buffer is written
+// again only two scans later, after a barrier every thread passed once done reading it,
+// so each scan needs one barrier.
+struct WaveTotals {
+  int4 buf[2][kPlanThreads / 64];
+};
+
+// Block-wide exclusive scan of four counters at once; *total gets the block sums.
+__device__ int4 block_exclusive_scan4(int4 v, WaveTotals& wt, int& turn, int4* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int4* t4 = wt.buf[turn];
+  turn ^= 1;
+  const int4 x = make_int4(wave_incl_scan<false>(v.x), wave_incl_scan<false>(v.y), wave_incl_scan<false>(v.z),
+                           wave_incl_scan<false>(v.w));
+  if (lane == 63) t4[w] = x;
+  __syncthreads();
+  int4 pre = make_int4(0, 0, 0, 0), tot = make_int4(0, 0, 0, 0);
+  for (int i = 0; i < nw; ++i) {
+    const int4 t = t4[i];
+    if (i < w) pre = make_int4(pre.x + t.x, pre.y + t.y, pre.z + t.z, pre.w + t.w);
+    tot = make_int4(tot.x + t.x, tot.y + t.y, tot.z + t.z, tot.w + t.w);
+  }
+  *total = tot;
+  return make_int4(pre.x + x.x - v.x, pre.y + x.y - v.y, pre.z + x.z - v.z, pre.w + x.w - v.w);
+}
+
+// Block-wide sum of v and max of m.
+__device__ int2 block_sum_max(int v, int m, WaveTotals& wt, int& turn) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int4* t4 = wt.buf[turn];
+  turn ^= 1;
+  const int sv = __builtin_amdgcn_readlane(wave_incl_scan<false>(v), 63);
+  const int mv = __builtin_amdgcn_readlane(wave_incl_scan<true>(m), 63);
+  if (lane == 0) t4[w] = make_int4(sv, mv, 0, 0);
+  __syncthreads();
+  int s = 0, mx = INT32_MIN;
+  for (int i = 0; i < nw; ++i) {
+    s += t4[i].x;
+    mx = max(mx, t4[i].y);
+  }
+  return make_int2(s, mx);
+}
+
+// Work planner: one workgroup. Each sequence is a decode row (n == 1: one work item per
+// 256-key split) or a chunk (n >= 2: row blocks of rows_per_item rows, each one work item
+// per head quad, or several when the tick's chunk items alone would not fill the GPU
+// and blocks are split over their key tiles; see chunk_split_tiles / refine_split_tiles).
+//
+// The row blocks of all chunks are listed in LDS once (kPlanBlocks at most, over at most
+// kPlanChunkSeqs chunk sequences), in the order their items are emitted: sequences in
+// order, each sequence's blocks from the last to the first (later blocks see more keys
+// under a causal mask, so they start first). Every pass over them runs on all threads:
+// the split-size search sums split counts over the list, and a scan over the list gives
+// each block its item, partial-slot and combine-record offsets. Larger ticks take the
+// serial walk (plan_serial), which produces the same lists.
+constexpr int kPlanChunkSeqs = 1024;
+constexpr int kPlanBlocks = 4096;
+constexpr int kPlanSearchWork = 1 << 16;  // candidates x blocks evaluated in one pass
+
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
+  __shared__ int wave_tot[kPlanThreads / 64];
+  __shared__ WaveTotals wt;
+  __shared__ int err_bits;
+  __shared__ int cand_wgs[kPlanThreads];  // split-size search: workgroups per candidate
+  __shared__ int best_st;
+  // Chunk sequence k: its sequence index, first row, clamped (n, L), first flat block, and its item /
+  // combine-record / partial-slot offsets once known.
+  __shared__ int cs_b[kPlanChunkSeqs], cs_q0[kPlanChunkSeqs], cs_n[kPlanChunkSeqs], cs_L[kPlanChunkSeqs];
+  __shared__ int cs_first[kPlanChunkSeqs + 1];
+  __shared__ int cs_off_p[kPlanChunkSeqs], cs_off_c[kPlanChunkSeqs], cs_off_s[kPlanChunkSeqs];
+  // Flat block i: key tiles, then (after the split) its offsets within the flat order.
+  __shared__ int fb_tiles[kPlanBlocks], fb_p[kPlanBlocks + 1], fb_c[kPlanBlocks + 1], fb_s[kPlanBlocks + 1];
+  const int tid = threadIdx.x;
+  if (tid == 0) {  // published by the barrier of phase 0's scan
+    err_bits = 0;
+    best_st = INT32_MAX;
+  }
+  int err = 0;
+  int turn = 0;  // WaveTotals buffer of the next block-wide scan
+
+  // Phase 0: list the chunk sequences and count their row blocks. A batch of one round
+  // keeps each thread's sequence metadata and chunk sequence index for phase 4.
+  int n_cs = 0, n_blk = 0;
+  SeqMeta m_kept{0, 0, 0, 0};
+  int k_kept = 0;
+  for (int b0 = 0; b0 < a.batch; b0 += kPlanThreads) {
+    const int b = b0 + tid;
+    SeqMeta m{0, 0, 0, 0};
+    if (b < a.batch) m = plan_seq(a, b, err);
+    m_kept = m;
+    const int is_chunk = b < a.batch && m.n >= 2;
+    const int nblk = is_chunk ? (m.n + a.rows_per_item - 1) / a.rows_per_item : 0;
+    int4 tot;
+    const int4 pre = block_exclusive_scan4(make_int4(is_chunk, nblk, 0, 0), wt, turn, &tot);
+    const int k = n_cs + pre.x;
+    k_kept = k;
+    if (is_chunk && k < kPlanChunkSeqs) {
+      cs_b[k] = b;
+      cs_q0[k] = m.q0;
+      cs_n[k] = m.n;
+      cs_L[k] = m.L;
+      cs_first[k] = n_blk + pre.y;
+    }
+    n_cs += tot.x;
+    n_blk += tot.y;
+  }
+  if (n_cs > kPlanChunkSeqs || n_blk > kPlanBlocks) {
+    int4 totals;
+    plan_serial(a, wave_tot, &err_bits, &totals);
+    if (err) atomicOr(&err_bits, err);
+    __syncthreads();
+    if (tid == 0) write_plan_header(a, err_bits, totals);
+    return;
+  }
+  if (tid == 0) cs_first[n_cs] = n_blk;
+  __syncthreads();
+
+  // Flat block i -> chunk sequence k (the last k with cs_first[k] <= i) and row block.
+  auto block_of = [&](int i, int& k, int& blk) {
+    int lo = 0, hi = n_cs - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (cs_first[mid] <= i) lo = mid;
+      else hi = mid - 1;
+    }
+    k = lo;
+    const int nblk = cs_first[k + 1] - cs_first[k];
+    blk = nblk - 1 - (i - cs_first[k]);
+  };
+
+  // Phase 1: key tiles of every block; totals before splitting. (The chunk-free branches
+  // below are workgroup-uniform.)
+  int2 tm = make_int2(0, 0);
+  if (n_blk > 0) {
+    int my_tiles = 0, my_max = 0;
+    for (int i = tid; i < n_blk; i += kPlanThreads) {
+      int k, blk;
+      block_of(i, k, blk);
+      int tb, te;
+      chunk_tiles(cs_n[k], cs_L[k], blk * a.rows_per_item, a.rows_per_item, a.win_left, a.win_right, &tb, &te);
+      fb_tiles[i] = te - tb;
+      my_tiles += te - tb;
+      my_max = max(my_max, te - tb);
+    }
+    tm = block_sum_max(my_tiles, my_max, wt, turn);  // its barrier publishes fb_tiles
+  }
+  const int64_t pf_items0 = (int64_t)n_blk * a.head_quads;
+  const int64_t pf_tiles = (int64_t)tm.x * a.head_quads;
+
+  // Phase 2: split size, as refine_split_tiles (the host count uses that). wgs(st) is
+  // non-increasing, so its binary search finds the smallest st in (st0, max] whose
+  // workgroups fit the target; when candidates x blocks is small, every candidate is
+  // evaluated at once (one per thread) and the smallest fitting one taken.
+  auto chunk_wgs = [&](int st) -> int64_t {
+    int wg = 0;
+    for (int i = tid; i < n_blk; i += kPlanThreads) wg += chunk_split_count(fb_tiles[i], st);
+    return (int64_t)block_sum_max(wg, 0, wt, turn).x * a.head_quads * a.hkv;
+  };
+  const int st0 = chunk_split_tiles(pf_tiles, pf_items0, a.hkv);
+  int split_tiles = st0;
+  if (st0 > 0 && tm.y > st0) {
+    const int ncand = tm.y - st0;  // candidates st0 + 1 .. max tiles
+    if (ncand < kPlanThreads && (int64_t)(ncand + 1) * n_blk <= kPlanSearchWork) {
+      // Thread j <= ncand counts the workgroups at split size st0 + j; the smallest
+      // fitting candidate wins an LDS atomicMin.
+      if (tid <= ncand) {
+        int wg = 0;
+        for (int i = 0; i < n_blk; ++i) wg += chunk_split_count(fb_tiles[i], st0 + tid);
+        cand_wgs[tid] = wg;
+      }
+      __syncthreads();
+      const int64_t w0 = (int64_t)cand_wgs[0] * a.head_quads * a.hkv;
+      const int64_t rounds = w0 / kChunkCUs;
+      if (rounds >= 1 && w0 % kChunkCUs != 0) {
+        if (tid >= 1 && tid <= ncand && (int64_t)cand_wgs[tid] * a.head_quads * a.hkv <= rounds * kChunkCUs)
+          atomicMin(&best_st, st0 + tid);
+        __syncthreads();
+        if (best_st != INT32_MAX) split_tiles = best_st;
+      }
+    } else {
+      split_tiles = refine_split_tiles(st0, tm.y, chunk_wgs);
+    }
+  }
+
+  // Phase 3: per block, items (S per head quad), partial rows (rows * S when split) and
+  // combine records (one per kCombRows split rows); exclusive scans in flat order.
+  if (n_blk > 0) {
+    int base_p = 0, base_c = 0, base_s = 0;
+    for (int i0 = 0; i0 < n_blk; i0 += kPlanThreads) {
+      const int i = i0 + tid;
+      int4 v = make_int4(0, 0, 0, 0);
+      if (i < n_blk) {
+        int k, blk;
+        block_of(i, k, blk);
+        const int S = chunk_split_count(fb_tiles[i], split_tiles);
+        const int rows = min(a.rows_per_item, cs_n[k] - blk * a.rows_per_item);
+        v.x = S * a.head_quads;
+        if (S > 1) {
+          v.y = (rows + kCombRows - 1) / kCombRows;
+          v.z = rows * S;
+        }
+      }
+      int4 tot;
+      const int4 pre = block_exclusive_scan4(v, wt, turn, &tot);
+      if (i < n_blk) {
+        fb_p[i] = base_p + pre.x;
+        fb_c[i] = base_c + pre.y;
+        fb_s[i] = base_s + pre.z;
+      }
+      base_p += tot.x;
+      base_c += tot.y;
+      base_s += tot.z;
+    }
+    if (tid == 0) {
+      fb_p[n_blk] = base_p;
+      fb_c[n_blk] = base_c;
+      fb_s[n_blk] = base_s;
+    }
+    __syncthreads();
+  }
+
+  // Phase 4: per sequence, item counts and offsets; decode items and sequence info.
+  int base_dec = 0, base_pf = 0, base_comb = 0, base_slot = 0;
+  int kc = 0;  // chunk sequences before this b0 round
+  for (int b0 = 0; b0 < a.batch; b0 += kPlanThreads) {
+    const int b = b0 + tid;
+    const bool active = b < a.batch;
+    SeqMeta m = m_kept;
+    if (active && a.batch > kPlanThreads) m = plan_seq(a, b, err);
+    const int is_chunk = active && m.n >= 2;
+    int4 cnt = make_int4(0, 0, 0, 0);  // decode items, chunk items, combine records, slots
+    int s_first = 0, splits = 0;
+    if (active && m.n == 1) {
+      decode_splits(m.L, a.win_left, &s_first, &splits);
+      cnt.x = splits;
+      cnt.z = splits > 1 ? 1 : 0;
+    }
+    // The chunk sequence index of b: the same compaction as phase 0.
+    int k = k_kept;
+    if (n_cs > 0 && a.batch > kPlanThreads) {
+      int4 ctot;
+      k = kc + block_exclusive_scan4(make_int4(is_chunk, 0, 0, 0), wt, turn, &ctot).x;
+      kc += ctot.x;
+    }
+    if (is_chunk) {
+      const int f0 = cs_first[k], f1 = cs_first[k + 1];
+      cnt.y = fb_p[f1] - fb_p[f0];
+      cnt.z = fb_c[f1] - fb_c[f0];
+      cnt.w = fb_s[f1] - fb_s[f0];
+    }
+    int4 tot;
+    const int4 pre = block_exclusive_scan4(cnt, wt, turn, &tot);
+    const int off_d = base_dec + pre.x, off_p = base_pf + pre.y;
+    const int off_c = base_comb + pre.z, off_s = base_slot + pre.w;
+    if (active) {
+      a.seq_info[b] = make_int4(m.q0, m.n, m.L, m.kvb);
+      for (int j = 0; j < cnt.x; ++j) {
+        if (off_d + j < a.max_dec) a.dec_items[off_d + j] = make_int4(b, s_first + j, m.q0, m.L);
+      }
+      if (cnt.z && m.n == 1 && off_c < a.max_comb) a.comb_seqs[off_c] = make_int4(b, off_d, splits, m.q0);
+      if (is_chunk) {
+        cs_off_p[k] = off_p;
+        cs_off_c[k] = off_c;
+        cs_off_s[k] = off_s;
+      }
+    }
+    base_dec += tot.x;
+    base_pf += tot.y;
+    base_comb += tot.z;
+    base_slot += tot.w;
+  }
+  __syncthreads();
+
+  // Phase 5: chunk items, their first partial rows, and combine records, one block per
+  // thread. A split block's rows own S consecutive partial slots each; its combine
+  // records cover kCombRows rows each.
+  for (int i = tid; i < n_blk; i += kPlanThreads) {
+    int k, blk;
+    block_of(i, k, blk);
+    const int f0 = cs_first[k];
+    const int b = cs_b[k], n = cs_n[k];
+    const int row0 = blk * a.rows_per_item;
+    const int S = chunk_split_count(fb_tiles[i], split_tiles);
+    const int rows = min(a.rows_per_item, n - row0);
+    const int item0 = cs_off_p[k] + fb_p[i] - fb_p[f0];
+    const int slot = cs_off_s[k] + fb_s[i] - fb_s[f0];
+    const int comb0 = cs_off_c[k] + fb_c[i] - fb_c[f0];
+    const bool fits = S == 1 || slot + rows * S <= a.cslot_cap;
+    if (!fits) err |= HX_WERR_GRID;
+    for (int hq = 0, j = 0; hq < a.head_quads; ++hq) {
+      for (int sp = 0; sp < S; ++sp, ++j) {
+        if (item0 + j < a.max_pf) {
+          a.pf_items[item0 + j] = make_int4(b, row0, hq, fits ? (sp | ((S - 1) << 16)) : 0);
+          a.pf_base[item0 + j] = slot;
+        }
+      }
+    }
+    if (S > 1) {
+      const int q0 = cs_q0[k];
+      for (int r = 0, comb = comb0; r < rows; r += kCombRows, ++comb) {
+        const int nr = min(kCombRows, rows - r);
+        if (fits && comb < a.max_comb)
+          a.comb_seqs[comb] = make_int4(b, (int)a.max_dec + slot + r * S, S | ((nr - 1) << 24), q0 + row0 + r);
+      }
+    }
+  }
   if (err) atomicOr(&err_bits, err);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int e = err_bits;
-    if (base_dec > a.max_dec || base_pf > a.max_pf || base_comb > a.max_comb) e |= HX_WERR_GRID;
-    a.hdr[H_NDEC] = base_dec < a.max_dec ? base_dec : (int)a.max_dec;
-    a.hdr[H_NPF] = base_pf < a.max_pf ? base_pf : (int)a.max_pf;
-    a.hdr[H_NCOMB] = base_comb < a.max_comb ? base_comb : (int)a.max_comb;
-    a.hdr[H_ERR] = e;
-    a.hdr[H_BATCH] = a.batch;
-    a.hdr[H_MAXQ] = a.max_q;
-    a.hdr[H_MAXK] = a.max_k;
-    a.hdr[H_HQ] = a.hq;
-    a.hdr[H_HKV] = a.hkv;
-    a.hdr[H_STAMP] = kPlanStamp;
-  }
+  if (tid == 0) write_plan_header(a, err_bits, make_int4(base_dec, base_pf, base_comb, base_slot));
 }
 
 // ------------------------------------------------------------------ run arguments
