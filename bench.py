@@ -115,19 +115,20 @@ class DecodeBench:
         self.ops = ops
 
     def step(self, layer: int, events=None):
-        """Append the new rows and attend, as PagedBatchCache.attend does. Decode-only
-        ticks append inside the decode kernel; ticks with chunk rows append first.
-        events[0..3] bracket (append, decode, combine + chunk)."""
+        """Append the new rows and attend, as PagedBatchCache.attend does. The decode
+        launch appends: decode rows inside their split workgroups, and on a tick with
+        chunk rows every row in workgroups added to that launch. A tick without decode
+        rows appends first. events[0..3] bracket (append, decode, combine + chunk)."""
         kp, vp = self.k_pools[layer], self.v_pools[layer]
-        fused = self.w.max_q == 1
+        in_decode = self.plan.hints[0] != 0
         if events is not None:
             events[0].record()
-        if not fused:
+        if not in_decode:
             self.ops.kv_append(kp, vp, self.slots, self.k_new, self.v_new)
         if events is not None:
             events[1].record()
         self.plan.run(self.q, kp, vp, self.block_table, out=self.out, phases=("decode",),
-                      append=(self.k_new, self.v_new, self.slots) if fused else None)
+                      append=(self.k_new, self.v_new, self.slots) if in_decode else None)
         if events is not None:
             events[2].record()
         self.plan.run(self.q, kp, vp, self.block_table, out=self.out, phases=("combine", "chunk"))
@@ -135,11 +136,12 @@ class DecodeBench:
             events[3].record()
 
     def phase(self, layer: int, name: str):
-        """One kernel of the step alone: the decode kernel (with its fused append on a
-        decode-only tick), the chunk kernel or the combine kernel."""
+        """One kernel of the step alone: the decode kernel (with the appends of the step;
+        "decode_only" without them), the chunk kernel or the combine kernel."""
         kp, vp = self.k_pools[layer], self.v_pools[layer]
-        fused = name == "decode" and self.w.max_q == 1
-        self.plan.run(self.q, kp, vp, self.block_table, out=self.out, phases=(name,),
+        fused = name == "decode" and self.plan.hints[0] != 0
+        self.plan.run(self.q, kp, vp, self.block_table, out=self.out,
+                      phases=("decode",) if name == "decode_only" else (name,),
                       append=(self.k_new, self.v_new, self.slots) if fused else None)
 
     def append(self, layer: int):
@@ -283,8 +285,8 @@ def packed_tick(device, steps: int = 30, warmup: int = 5):
     assert b.plan.error_word() == 0, "attention plan reported an error"
     # per-kernel device time, each kernel's launches replayed from a HIP graph
     us = {name: graph_time_us([lambda i=i, name=name: b.phase(i, name) for i in range(2)], steps)
-          for name in ("decode", "chunk", "combine")}
-    us["append"] = graph_time_us([lambda i=i: b.append(i) for i in range(2)], steps)
+          for name in ("decode", "decode_only", "chunk", "combine")}
+    us["append_separate"] = graph_time_us([lambda i=i: b.append(i) for i in range(2)], steps)
     res = {
         "workload": "c3: 32 decoders ctx U[1024,4096] + chunks 1024@0 and 992@512, bf16",
         "tokens": w.total_q,
@@ -292,8 +294,8 @@ def packed_tick(device, steps: int = 30, warmup: int = 5):
         "tick_ms_36_layers": round(sec * N_LAYERS_MODEL * 1e3, 3),
         "tokens_per_s_attention_only": round(w.total_q / (sec * N_LAYERS_MODEL), 1),
         "kernel_us": {k: round(v, 2) for k, v in us.items()},
-        "decode_rows_us": round(us["decode"], 2),
-        "decode_rows_gbs": round(w.decode_bytes() / (us["decode"] * 1e-6) / 1e9, 1),
+        "decode_rows_us": round(us["decode_only"], 2),
+        "decode_rows_gbs": round(w.decode_bytes() / (us["decode_only"] * 1e-6) / 1e9, 1),
         "chunk_rows_us": round(us["chunk"] + us["combine"], 2),
         "chunk_kernel_tflops": round(w.chunk_flops() / (us["chunk"] * 1e-6) / 1e12, 1),
         "chunk_kernel_mfma_frac": round(w.chunk_flops() / (us["chunk"] * 1e-6) / 2.5e15, 4),
@@ -319,7 +321,8 @@ def long_context(device, steps: int = 10, warmup: int = 3):
     torch.cuda.synchronize()
     assert b.plan.error_word() == 0, "attention plan reported an error"
     append_us = graph_time_us([lambda: b.append(0)], steps)
-    decode_us = graph_time_us([lambda: b.phase(0, "decode")], steps)
+    decode_us = graph_time_us([lambda: b.phase(0, "decode_only")], steps)
+    decode_append_us = graph_time_us([lambda: b.phase(0, "decode")], steps)
     chunk_kernel_us = graph_time_us([lambda: b.phase(0, "chunk")], steps)
     combine_us = graph_time_us([lambda: b.phase(0, "combine")], steps)
     chunk_us = chunk_kernel_us + combine_us
@@ -368,6 +371,7 @@ def long_context(device, steps: int = 10, warmup: int = 3):
                     "positions 4096-8191; restore of 16 prefix pages x 36 layers x K/V",
         "append_us": round(append_us, 2),
         "decode_rows_us": round(decode_us, 2),
+        "decode_launch_with_all_appends_us": round(decode_append_us, 2),
         "decode_rows_gbs_unique": round(w.decode_bytes() / (decode_us * 1e-6) / 1e9, 1),
         "chunk_rows_us": round(chunk_us, 2),
         "chunk_kernel_us": round(chunk_kernel_us, 2),

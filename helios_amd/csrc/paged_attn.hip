@@ -56,6 +56,7 @@ constexpr int kChunkCUs = 256;  // CUs of an MI355X
 constexpr int kMinSplitTiles = 8;
 constexpr int kMaxChunkSplits = 64;
 constexpr int kCombRows = 8;  // output rows per combine record of a split chunk block
+constexpr int kAppendWGs = 256;  // append workgroups in a decode launch, at most
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -808,6 +809,9 @@ struct RunArgs {
   const int64_t* write_slots;
   int64_t kn_row, kn_head, vn_row, vn_head;  // element strides
   int64_t pool_rows;
+  // Workgroups after the decode workgroups of the decode launch that append every row of
+  // the tick (0: none; the chunk rows then went in by a separate append beforehand).
+  int32_t app_wgs;
 };
 
 // True when the workspace holds a plan for this run's shape; otherwise the block
@@ -893,7 +897,33 @@ __device__ __forceinline__ float wave_sum(float v) {
   return hx::add_xor32(hx::add_xor16(v));
 }
 
-template <typename T, int G>
+// The append workgroups of a decode launch: every row t of the tick goes to pool row
+// write_slots[t] (index_copy_ semantics; slots outside the pool are skipped), 16 bytes
+// per thread step. The chunk kernel, launched after this launch, reads the chunk rows;
+// a decode row's split workgroup also writes its own row (the same bits) and takes the
+// new token from k_new / v_new, never from the pool.
+template <typename T>
+__device__ void append_rows(const RunArgs& a, int wg, int n_wg) {
+  constexpr int kWords = kD / 8;  // 16-byte words per head row
+  const int64_t per_token = (int64_t)a.hkv * kWords;
+  const int64_t total = (int64_t)a.total_q * per_token;
+  for (int64_t idx = (int64_t)wg * kThreads + threadIdx.x; idx < total; idx += (int64_t)n_wg * kThreads) {
+    const int64_t t = idx / per_token;
+    const int rem = (int)(idx - t * per_token);
+    const int h = rem / kWords, w = rem - h * kWords;
+    const int64_t slot = a.write_slots[t];
+    if (slot < 0 || slot >= a.pool_rows) continue;
+    const uint4 kw = ld16(reinterpret_cast<const T*>(a.k_new) + t * a.kn_row + (int64_t)h * a.kn_head + 8 * w);
+    const uint4 vw = ld16(reinterpret_cast<const T*>(a.v_new) + t * a.vn_row + (int64_t)h * a.vn_head + 8 * w);
+    const int64_t off = (slot * a.kv_row + (int64_t)h * a.kv_head + 8 * w) * (int64_t)sizeof(T);
+    *reinterpret_cast<uint4*>(const_cast<uint8_t*>(a.k) + off) = kw;
+    *reinterpret_cast<uint4*>(const_cast<uint8_t*>(a.v) + off) = vw;
+  }
+}
+
+// APPEND_ROWS: the launch also holds the append workgroups (a.app_wgs after the decode
+// workgroups); a separate instantiation, so decode-only launches carry no trace of them.
+template <typename T, int G, bool APPEND_ROWS>
 __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
   typedef hx::Elem<T> E;
   constexpr int GP = G <= 4 ? 4 : 8;      // floats per token in p_lds
@@ -912,6 +942,13 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(RunArgs a) {
   // workgroups an XCD receives are the KV heads of one split; each XCD then streams whole
   // token rows of the pages it reads (about 4 % faster than one head per XCD). The grid
   // covers the work items rounded up to a multiple of kXcds.
+  if constexpr (APPEND_ROWS) {
+    const int dec_wgs = (a.grid_dec + kXcds - 1) / kXcds * kXcds * a.hkv;
+    if ((int)blockIdx.x >= dec_wgs) {  // append workgroups follow the decode workgroups
+      append_rows<T>(a, (int)blockIdx.x - dec_wgs, a.app_wgs);
+      return;
+    }
+  }
   const int xcd = (int)blockIdx.x % kXcds, jx = (int)blockIdx.x / kXcds;
   const int g = jx % a.hkv;
   const int item = (jx / a.hkv) * kXcds + xcd;
@@ -1804,8 +1841,12 @@ int64_t decode_grid(int64_t grid_dec) { return (grid_dec + kXcds - 1) / kXcds * 
 template <typename T, int G>
 int launch_run(const RunArgs& a, hipStream_t s) {
   // The combine merges decode and chunk split partials, so it runs last.
-  if (a.grid_dec > 0)
-    hipLaunchKernelGGL((decode_kernel<T, G>), dim3((unsigned)(decode_grid(a.grid_dec) * a.hkv)), dim3(kThreads), 0, s, a);
+  if (a.app_wgs > 0)
+    hipLaunchKernelGGL((decode_kernel<T, G, true>), dim3((unsigned)(decode_grid(a.grid_dec) * a.hkv + a.app_wgs)),
+                       dim3(kThreads), 0, s, a);
+  else if (a.grid_dec > 0)
+    hipLaunchKernelGGL((decode_kernel<T, G, false>), dim3((unsigned)(decode_grid(a.grid_dec) * a.hkv)), dim3(kThreads),
+                       0, s, a);
   if (a.grid_pf > 0)
     hipLaunchKernelGGL((chunk_kernel<T, G>), dim3((unsigned)(a.grid_pf * a.hkv)), dim3(kChunkThreads), 0, s, a);
   if (a.grid_comb > 0)
@@ -2066,13 +2107,14 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
   a.grid_dec = clamp_hint(decode_items_hint, l.max_dec);
   a.grid_pf = max_q >= 2 ? clamp_hint(prefill_items_hint, l.max_pf) : 0;
   a.grid_comb = clamp_hint(combine_seqs_hint, l.max_comb);
-  if (decode_grid(a.grid_dec) * n_kv_heads > INT32_MAX || (int64_t)a.grid_pf * n_kv_heads > INT32_MAX)
+  if (decode_grid(a.grid_dec) * n_kv_heads + kAppendWGs > INT32_MAX || (int64_t)a.grid_pf * n_kv_heads > INT32_MAX)
     return HX_E_INVALID_ARG;
   a.k_new = nullptr;
   a.v_new = nullptr;
   a.write_slots = nullptr;
   a.kn_row = a.kn_head = a.vn_row = a.vn_head = 0;
   a.pool_rows = 0;
+  a.app_wgs = 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int G = n_q_heads / n_kv_heads;
   const bool tuned = tuned_shape(G, head_dim);
@@ -2088,8 +2130,14 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
         app->kn_head < 0 || app->vn_row < 0 || app->vn_head < 0 || app->pool_rows < 0)
       return HX_E_INVALID_ARG;
     // Chunk rows (and every row of generic_kernel) read their own new keys from the
-    // pool: append every row first.
-    if (a.grid_pf > 0 || !tuned) {
+    // pool. When the tick may hold chunk rows and a decode launch runs on the tuned path,
+    // workgroups added to that launch write every row (the chunk kernel runs after it,
+    // also in a later call); otherwise every row is appended first when chunk rows run.
+    const bool append_in_decode = tuned && max_q >= 2 && a.grid_dec > 0;
+    if (append_in_decode) {
+      const int64_t wgs = ((int64_t)total_q * n_kv_heads * (head_dim / 8) + kThreads - 1) / kThreads;
+      a.app_wgs = (int32_t)(wgs < kAppendWGs ? wgs : kAppendWGs);
+    } else if (a.grid_pf > 0 || !tuned) {
       const int elem = 2;
       const int st2 = hx_kv_append(const_cast<void*>(k_cache), const_cast<void*>(v_cache), app->pool_rows,
                                    app->k_new, app->kn_row, app->kn_head, app->v_new, app->vn_row,

@@ -188,8 +188,9 @@ int hx_varlen_attn_run(const void* q, int64_t q_row_stride, int64_t q_head_strid
  * the new key / value of packed query row t. Decode rows are appended inside the
  * decode kernel (the workgroup owning the row's last split stores its head's slice
  * and uses it from registers), so a decode-only tick issues no separate append
- * launch; when chunk rows are present every row is appended first by the append
- * kernel. The pool must hold the token of decode row b at block-table position
+ * launch. On a tick that may hold chunk rows (max_q >= 2), workgroups added to the
+ * decode launch append every row, and the chunk kernel, launched after it, reads them;
+ * when no decode launch runs, every row is appended first by the append kernel. The pool must hold the token of decode row b at block-table position
  * seqused_k[b] - 1, i.e. write_slots must agree with the block table, as the
  * reference's metadata does by construction. pool_rows = num_pages * page_size. The
  * pools must be contiguous rows: kv_row_stride == n_kv_heads * head_dim and
