@@ -264,8 +264,9 @@ def test_validation_errors(device):
 
 @pytest.mark.parametrize("name", ["c1", "mixed", "c2", "c3"])
 def test_fused_append_matches_separate_calls(device, name):
-    """The fused append + attention call (decode rows appended inside the decode kernel,
-    chunk rows by the append kernel first) leaves the pools with the bits of a separate
+    """The fused append + attention call (decode rows appended inside the decode kernel;
+    on a tick with chunk rows, every row by workgroups added to the decode launch) leaves
+    the pools with the bits of a separate
     index_copy_-style append and returns the bits of attention on the appended pool, at
     the sizes the benchmark times (C2: 64 decode rows; C3: 32 decode rows + 2016 chunk
     rows); the fused output is also checked against the oracle (C3: every decode row and
@@ -356,3 +357,28 @@ def test_fused_append_ignores_stale_pool_rows(device):
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
     assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("name", ["mixed", "c3", "c4"])
+def test_phased_append_run_matches_one_call(device, name):
+    """The benchmark's step on a tick with chunk rows: the decode phase with append=
+    (its added workgroups write every row), then chunk and combine in a second call,
+    gives the pools and output bits of the fused single call."""
+    say("phased append", name)
+    w = {"c3": synth.c3, "c4": synth.c4}.get(name, lambda: synth.small_mixed(
+        81, batch=7, max_cached=1500, max_chunk=300, num_pages=64))()
+    ref = DeviceTick(w, torch.bfloat16, device, pool_on_device=name != "mixed")
+    app = (ref.k_new, ref.v_new, ref.write_slots)
+    k1, v1 = ref.fresh_pools()
+    plan = ref.plan()
+    out1 = plan.run(ref.q, k1, v1, ref.block_table, append=app)
+    k2, v2 = ref.fresh_pools()
+    out2 = torch.empty_like(out1)
+    plan.run(ref.q, k2, v2, ref.block_table, out=out2, phases=("decode",), append=app)
+    plan.run(ref.q, k2, v2, ref.block_table, out=out2, phases=("combine", "chunk"))
+    torch.cuda.synchronize()
+    assert plan.error_word() == 0
+    assert torch.equal(k2.view(torch.int16), k1.view(torch.int16))
+    assert torch.equal(v2.view(torch.int16), v1.view(torch.int16))
+    assert torch.equal(k1.view(torch.int16), ref.k_pool.view(torch.int16))
+    assert torch.equal(out2.view(torch.int16), out1.view(torch.int16))
