@@ -1336,6 +1336,13 @@ constexpr int kKStride = kD + 8;       // K tile row: 136 elements (272 B)
 constexpr int kVStride = kTile + 8;    // V^T tile row: 72 elements (144 B = 36 dwords)
 constexpr int kChunkThreads = 512;     // 8 waves: 2 per SIMD
 constexpr float kLazyLog2 = 8.f;       // softmax terms stay <= 2^8 between max updates
+// Output staging after the tile loop: each wave's 32 rows of one head (256 B each) at a
+// 288-byte stride (72 dwords: the 16 rows x 4 chunks one staging write covers fall on
+// distinct bank pairs), in the LDS the K / V tiles used.
+constexpr int kStageStride = 2 * kD + 32;
+constexpr int kTileLdsBytes = 2 * (kTile * kKStride + kD * kVStride);
+constexpr int kStageLdsBytes = 8 * 32 * kStageStride;
+constexpr int kChunkLdsBytes = kTileLdsBytes > kStageLdsBytes ? kTileLdsBytes : kStageLdsBytes;
 
 // V^T tile layout. Row d holds the 64 keys of dim d as 32 dwords (key pairs) in eight
 // 16-byte groups. Group 4*ks + q holds, in this order, keys 32ks + 4q + 0..3 and
@@ -1360,8 +1367,10 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   typedef hx::Elem<T> E;
   typedef typename E::v8 v8;
   constexpr int Gw = G < 4 ? G : 4;
-  __shared__ __attribute__((aligned(16))) T k_lds[kTile * kKStride];
-  __shared__ __attribute__((aligned(16))) T vt_lds[kD * kVStride];
+  // V^T first: its transposing writes pair up (ds_write2) only with small offsets.
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kChunkLdsBytes];
+  T* const vt_lds = reinterpret_cast<T*>(lds);
+  T* const k_lds = reinterpret_cast<T*>(lds + 2 * kD * kVStride);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, held in a scalar register
@@ -1621,41 +1630,57 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
     __syncthreads();
   }
 
-  // Normalise and store: lane holds dims 16db+4(lane>>4)+0..3 of row 16rb+(lane&15).
-  // A split writes its partial (m in log2 units, l, o / l) to the row's slot instead.
+  // Normalise: lane holds dims 16db+4(lane>>4)+0..3 of row 16rb+(lane&15). The rows go
+  // through this wave's LDS staging area and leave as whole 256-byte head rows, four per
+  // store instruction (writing the fragment layout directly scatters 32-byte pieces of
+  // 16 rows per instruction, about 2.5 us more per workgroup). A split writes its
+  // partial (m in log2 units, l, o / l) to the row's slot instead of the output.
+  // The tile loop ends with a barrier, so every wave is done with the tiles here.
   const int64_t slot0 = S > 1 ? a.dec_cap + a.pf_base[item] + sp : 0;
+  uint8_t* const stage = lds + w * (32 * kStageStride);
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
     const float l = hx::add_xor32(hx::add_xor16(l_run[rb]));
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint8_t* srow = stage + (16 * rb + (lane & 15)) * kStageStride + 8 * (lane >> 4);
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+      *reinterpret_cast<uint2*>(srow + 32 * db) =
+          make_uint2(hx::pack2_round<T>(oacc[db][rb][0] * inv, oacc[db][rb][1] * inv),
+                     hx::pack2_round<T>(oacc[db][rb][2] * inv, oacc[db][rb][3] * inv));
     const int rr = wr0 + 16 * rb + (lane & 15);
-    if (rr < n && S > 1) {
+    if (rr < n && (lane >> 4) == 0) {
+      if (S > 1) {
+        const int64_t slot = slot0 + (int64_t)(rr - row0) * S;
+        if (slot < a.slot_cap) a.part_ml[slot * a.hq + qh] = make_float2(l > 0.f ? m_run[rb] * sl2 : -INFINITY, l);
+      } else if (a.lse) {
+        a.lse[(int64_t)qh * a.total_q + q0 + rr] = l > 0.f ? (m_run[rb] * sl2 + log2f(l)) * kLn2 : -INFINITY;
+      }
+    }
+  }
+  __syncthreads();  // staged rows visible to the whole wave
+  // Lane (r4, c) = (lane >> 4, lane & 15) stores the 16-byte chunk c of staged row 4i + r4.
+  // Output rows are 16-byte aligned unless the caller's strides or pointer are only
+  // 8-byte aligned (allowed): then each chunk goes as two 8-byte stores.
+  const bool out16 = a.o_row % 8 == 0 && a.o_head % 8 == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int sr = 4 * i + (lane >> 4);
+    const int rr = wr0 + sr;
+    const uint4 u = *reinterpret_cast<const uint4*>(stage + sr * kStageStride + 16 * (lane & 15));
+    if (rr >= n) continue;
+    if (S > 1) {
       const int64_t slot = slot0 + (int64_t)(rr - row0) * S;
-      if (slot < a.slot_cap) {
-        const float inv = l > 0.f ? 1.f / l : 0.f;
-        uint16_t* prow = a.part_o + (slot * a.hq + qh) * kD;
-#pragma unroll
-        for (int db = 0; db < 8; ++db) {
-          const int d0 = 16 * db + 4 * (lane >> 4);
-          const uint2 u = make_uint2(hx::pack2_round<T>(oacc[db][rb][0] * inv, oacc[db][rb][1] * inv),
-                                     hx::pack2_round<T>(oacc[db][rb][2] * inv, oacc[db][rb][3] * inv));
-          *reinterpret_cast<uint2*>(prow + d0) = u;
-        }
-        if ((lane >> 4) == 0)
-          a.part_ml[slot * a.hq + qh] = make_float2(l > 0.f ? m_run[rb] * sl2 : -INFINITY, l);
+      if (slot < a.slot_cap) *reinterpret_cast<uint4*>(a.part_o + (slot * a.hq + qh) * kD + 8 * (lane & 15)) = u;
+    } else {
+      uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + (int64_t)(q0 + rr) * a.o_row + (int64_t)qh * a.o_head +
+                    8 * (lane & 15);
+      if (out16) {
+        *reinterpret_cast<uint4*>(o) = u;
+      } else {
+        reinterpret_cast<uint2*>(o)[0] = make_uint2(u.x, u.y);
+        reinterpret_cast<uint2*>(o)[1] = make_uint2(u.z, u.w);
       }
-    } else if (rr < n) {
-      const float inv = l > 0.f ? 1.f / l : 0.f;
-      uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + (int64_t)(q0 + rr) * a.o_row + (int64_t)qh * a.o_head;
-#pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        const int d0 = 16 * db + 4 * (lane >> 4);
-        const uint2 u = make_uint2(hx::pack2_round<T>(oacc[db][rb][0] * inv, oacc[db][rb][1] * inv),
-                                   hx::pack2_round<T>(oacc[db][rb][2] * inv, oacc[db][rb][3] * inv));
-        *reinterpret_cast<uint2*>(orow + d0) = u;
-      }
-      if (a.lse && (lane >> 4) == 0)
-        a.lse[(int64_t)qh * a.total_q + q0 + rr] =
-            l > 0.f ? (m_run[rb] * sl2 + log2f(l)) * kLn2 : -INFINITY;
     }
   }
 }
