@@ -1336,11 +1336,11 @@ constexpr int kKStride = kD + 8;       // K tile row: 136 elements (272 B)
 constexpr int kVStride = kTile + 8;    // V^T tile row: 72 elements (144 B = 36 dwords)
 constexpr int kChunkThreads = 512;     // 8 waves: 2 per SIMD
 constexpr float kLazyLog2 = 8.f;       // softmax terms stay <= 2^8 between max updates
-// Output staging after the tile loop: each wave's 32 rows of one head (256 B each) at a
-// 288-byte stride (72 dwords: the 16 rows x 4 chunks one staging write covers fall on
-// distinct bank pairs), in the LDS the K / V tiles used.
+// Tile buffers: two K and two V^T tiles. Output staging after the tile loop: each
+// wave's 32 rows of one head (256 B each) at a 288-byte stride (72 dwords: the 16 rows x
+// 4 chunks one staging write covers fall on distinct bank pairs), in the same LDS.
 constexpr int kStageStride = 2 * kD + 32;
-constexpr int kTileLdsBytes = 2 * (kTile * kKStride + kD * kVStride);
+constexpr int kTileLdsBytes = 2 * 2 * (kTile * kKStride + kD * kVStride);
 constexpr int kStageLdsBytes = 8 * 32 * kStageStride;
 constexpr int kChunkLdsBytes = kTileLdsBytes > kStageLdsBytes ? kTileLdsBytes : kStageLdsBytes;
 
@@ -1361,16 +1361,20 @@ __device__ __forceinline__ int vt_col(int kp, int dblk) {
 // heads of KV head g). Wave w owns 32 rows (two 16-row MFMA blocks) of head w % Gw.
 // Each 64-key tile of K (row-major) and V (transposed as above) goes through LDS once
 // and feeds all 8 waves; the next tile is prefetched into registers while the current
-// one is consumed. Two waves per SIMD hide each other's LDS and memory latency.
+// one is consumed. Tiles alternate between two LDS buffers, so one barrier per tile
+// (after the registers are staged) suffices: a buffer is written again two tiles later,
+// after every wave has passed the barrier that follows its last read. Two waves per
+// SIMD hide each other's LDS and memory latency.
 template <typename T, int G>
 __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   typedef hx::Elem<T> E;
   typedef typename E::v8 v8;
   constexpr int Gw = G < 4 ? G : 4;
-  // V^T first: its transposing writes pair up (ds_write2) only with small offsets.
+  // V^T buffers first: their transposing writes pair up (ds_write2) only with small
+  // offsets.
   __shared__ __attribute__((aligned(16))) uint8_t lds[kChunkLdsBytes];
-  T* const vt_lds = reinterpret_cast<T*>(lds);
-  T* const k_lds = reinterpret_cast<T*>(lds + 2 * kD * kVStride);
+  T* const vt_lds = reinterpret_cast<T*>(lds);                          // two V^T tiles
+  T* const k_lds = reinterpret_cast<T*>(lds + 2 * 2 * kD * kVStride);    // two K tiles
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, held in a scalar register
@@ -1504,15 +1508,18 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
 
   if (t_begin < t_end) load_tile(t_begin);
   for (int t = t_begin; t < t_end; ++t) {
+    const int hb = (t - t_begin) & 1;
+    T* const kl = k_lds + hb * (kTile * kKStride);
+    T* const vl = vt_lds + hb * (kD * kVStride);
     // Registers -> LDS: K row-major, V transposed (pairs of keys packed per 32-bit word).
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-      *reinterpret_cast<uint4*>(&k_lds[(kr_base + 32 * j) * kKStride + 8 * c16]) = kreg[j];
+      *reinterpret_cast<uint4*>(&kl[(kr_base + 32 * j) * kKStride + 8 * c16]) = kreg[j];
     {
       const uint4 x = vreg[0], y = vreg[1];
       const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
       const uint32_t ys[4] = {y.x, y.y, y.z, y.w};
-      uint32_t* vt32 = reinterpret_cast<uint32_t*>(vt_lds);
+      uint32_t* vt32 = reinterpret_cast<uint32_t*>(vl);
 #pragma unroll
       for (int wd = 0; wd < 4; ++wd) {
         const int d = 8 * c16 + 2 * wd;
@@ -1535,7 +1542,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
         const uint4 af = *reinterpret_cast<const uint4*>(
-            &k_lds[(16 * kb + (lane & 15)) * kKStride + 32 * st + 8 * (lane >> 4)]);
+            &kl[(16 * kb + (lane & 15)) * kKStride + 32 * st + 8 * (lane >> 4)]);
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
           sacc[kb][rb] = E::mfma16x16x32(hx::as_v8<T>(af), hx::as_v8<T>(qf[rb][st]), sacc[kb][rb]);
@@ -1620,14 +1627,13 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
 #pragma unroll
       for (int db = 0; db < 8; ++db)
         vf[db] = *reinterpret_cast<const uint4*>(
-            &vt_lds[(16 * db + (lane & 15)) * kVStride + 8 * ((4 * ks + (lane >> 4)) ^ db)]);
+            &vl[(16 * db + (lane & 15)) * kVStride + 8 * ((4 * ks + (lane >> 4)) ^ db)]);
 #pragma unroll
       for (int db = 0; db < 8; ++db)
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
           oacc[db][rb] = E::mfma16x16x32(hx::as_v8<T>(vf[db]), pb[ks][rb], oacc[db][rb]);
     }
-    __syncthreads();
   }
 
   // Normalise: lane holds dims 16db+4(lane>>4)+0..3 of row 16rb+(lane&15). The rows go
@@ -1635,9 +1641,9 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   // store instruction (writing the fragment layout directly scatters 32-byte pieces of
   // 16 rows per instruction, about 2.5 us more per workgroup). A split writes its
   // partial (m in log2 units, l, o / l) to the row's slot instead of the output.
-  // The tile loop ends with a barrier, so every wave is done with the tiles here.
   const int64_t slot0 = S > 1 ? a.dec_cap + a.pf_base[item] + sp : 0;
   uint8_t* const stage = lds + w * (32 * kStageStride);
+  __syncthreads();  // every wave is done with the tiles
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
     const float l = hx::add_xor32(hx::add_xor16(l_run[rb]));
