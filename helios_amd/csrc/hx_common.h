@@ -8,6 +8,17 @@
 
 namespace hx {
 
+// Work-item and workgroup indices and sizes along x, read with the intrinsics. HIP's
+// threadIdx / blockIdx / blockDim / gridDim go through device-library functions built for
+// IEEE mode, which the inliner keeps out of these non-IEEE kernels: every use was a real
+// call, and a kernel that calls gives up registers to the calling convention.
+__device__ __forceinline__ int tid_x() { return (int)__builtin_amdgcn_workitem_id_x(); }
+__device__ __forceinline__ int wg_x() { return (int)__builtin_amdgcn_workgroup_id_x(); }
+__device__ __forceinline__ int wg_size_x() { return (int)__builtin_amdgcn_workgroup_size_x(); }
+__device__ __forceinline__ int num_wg_x() {
+  return (int)(__builtin_amdgcn_grid_size_x() / __builtin_amdgcn_workgroup_size_x());
+}
+
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));

@@ -30,8 +30,8 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   const int64_t per_token = (int64_t)a.n_kv * a.words;
   const int64_t total = a.n_tokens * per_token;
   const int64_t pool_row_b = (int64_t)a.n_kv * a.head_b;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
+  for (int64_t idx = (int64_t)hx::wg_x() * hx::wg_size_x() + hx::tid_x(); idx < total;
+       idx += (int64_t)hx::num_wg_x() * hx::wg_size_x()) {
     const int64_t t = idx / per_token;
     const int rem = (int)(idx - t * per_token);
     const int h = rem / a.words;
@@ -83,7 +83,7 @@ struct CopyArgs {
 // (the first form of this kernel) reached only ~2.6 TB/s.
 __global__ __launch_bounds__(kCopyThreads) void kv_copy_pages_kernel(CopyArgs a) {
   const int64_t total = (int64_t)a.n_tensors * a.n_pages * a.tiles_per_page;
-  for (int64_t t = blockIdx.x; t < total; t += gridDim.x) {
+  for (int64_t t = hx::wg_x(); t < total; t += hx::num_wg_x()) {
     const int tile = (int)(t % a.tiles_per_page);
     const int64_t rest = t / a.tiles_per_page;
     const int pair = (int)(rest % a.n_pages);
@@ -95,14 +95,14 @@ __global__ __launch_bounds__(kCopyThreads) void kv_copy_pages_kernel(CopyArgs a)
     hx::u32x4_t buf[kCopyDepth];
 #pragma unroll
     for (int i = 0; i < kCopyDepth; ++i) {
-      const int64_t off = t0 + ((int64_t)i * kCopyThreads + threadIdx.x) * 16;
+      const int64_t off = t0 + ((int64_t)i * kCopyThreads + hx::tid_x()) * 16;
       buf[i] = off < a.page_bytes
                    ? __builtin_nontemporal_load(reinterpret_cast<const hx::u32x4_t*>(src + off))
                    : hx::u32x4_t{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int i = 0; i < kCopyDepth; ++i) {
-      const int64_t off = t0 + ((int64_t)i * kCopyThreads + threadIdx.x) * 16;
+      const int64_t off = t0 + ((int64_t)i * kCopyThreads + hx::tid_x()) * 16;
       if (off < a.page_bytes) __builtin_nontemporal_store(buf[i], reinterpret_cast<hx::u32x4_t*>(dst + off));
     }
   }
@@ -126,8 +126,8 @@ template <typename W>
 __global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
   const int64_t per_head = a.length * a.words;
   const int64_t total = (int64_t)a.n_kv * per_head;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
+  for (int64_t idx = (int64_t)hx::wg_x() * hx::wg_size_x() + hx::tid_x(); idx < total;
+       idx += (int64_t)hx::num_wg_x() * hx::wg_size_x()) {
     const int h = (int)(idx / per_head);
     const int64_t rem = idx - (int64_t)h * per_head;
     const int64_t j = rem / a.words;
@@ -154,7 +154,7 @@ constexpr int kGatherRows = 32;
 
 template <int RW, int HW>
 __global__ __launch_bounds__(256) void kv_gather_rows_kernel(GatherArgs a) {
-  const int64_t tok0 = (int64_t)blockIdx.x * kGatherRows;
+  const int64_t tok0 = (int64_t)hx::wg_x() * kGatherRows;
   const int rows = (int)min((int64_t)kGatherRows, a.length - tok0);
   const int32_t page = a.pages[tok0 / a.page_size];
   const bool ok = page >= 0 && page < a.num_pool_pages;
@@ -165,12 +165,12 @@ __global__ __launch_bounds__(256) void kv_gather_rows_kernel(GatherArgs a) {
   hx::u32x4_t v[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    const int q = threadIdx.x + 256 * i;
+    const int q = hx::tid_x() + 256 * i;
     v[i] = (ok && q / RW < rows) ? __builtin_nontemporal_load(src + q) : hx::u32x4_t{0u, 0u, 0u, 0u};
   }
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    const int q = threadIdx.x + 256 * i;
+    const int q = hx::tid_x() + 256 * i;
     const int jr = q / RW, wr = q & (RW - 1);
     if (jr < rows)
       __builtin_nontemporal_store(v[i], out + ((int64_t)(wr / HW) * a.length + tok0 + jr) * HW + (wr & (HW - 1)));

@@ -65,7 +65,7 @@ __global__ __launch_bounds__(kLgThreads) void final_norm_kernel(
     const uint16_t* x, int64_t x_row, int64_t total_rows, const int64_t* idx, int64_t n,
     const float* w, float eps, int hidden, uint16_t* xn, int32_t* row_ok) {
   __shared__ float s_part[kLgThreads / 64];
-  const int j = blockIdx.x, tid = threadIdx.x;
+  const int j = hx::wg_x(), tid = hx::tid_x();
   const int nv = hidden >> 3;
   uint4* dst = reinterpret_cast<uint4*>(xn + (int64_t)j * hidden);
   int64_t src = -1;
@@ -145,8 +145,8 @@ __global__ __launch_bounds__(kLgThreads) void logits_argmax_kernel(
   __shared__ __attribute__((aligned(16))) unsigned char s_x[NT * 16 * kLgRowBytes];
   __shared__ uint64_t s_key[kLgThreads / 64][NT * 16];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t v0 = (int64_t)blockIdx.x * kLgVocabTile;
+  const int tid = hx::tid_x(), lane = tid & 63, wave = tid >> 6;
+  const int64_t v0 = (int64_t)hx::wg_x() * kLgVocabTile;
 
   // Global source of this thread's weight loads: rows past the vocab re-read the last
   // row (their logits are never used).
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(kLgThreads) void logits_argmax_kernel(
   __syncthreads();
   for (int j = tid; j < n; j += kLgThreads) {
     const uint64_t m = max_u64(max_u64(s_key[0][j], s_key[1][j]), max_u64(s_key[2][j], s_key[3][j]));
-    partial[(int64_t)j * tiles + blockIdx.x] = m;
+    partial[(int64_t)j * tiles + hx::wg_x()] = m;
   }
 }
 
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kLgThreads) void argmax_reduce_kernel(
     const uint64_t* partial, int32_t tiles, const int32_t* row_ok, int64_t* token_ids,
     float* max_logits) {
   __shared__ uint64_t s_best[kLgThreads / 64];
-  const int j = blockIdx.x, tid = threadIdx.x;
+  const int j = hx::wg_x(), tid = hx::tid_x();
   const uint64_t* p = partial + (int64_t)j * tiles;
   uint64_t best = 0;
   for (int t = tid; t < tiles; t += kLgThreads) best = max_u64(best, p[t]);

@@ -220,7 +220,7 @@ struct PlanArgs {
 };
 
 __device__ int block_exclusive_scan(int v, int* wave_tot, int* total) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int lane = hx::tid_x() & 63, w = hx::tid_x() >> 6, nw = hx::wg_size_x() >> 6;
   int x = v;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -314,11 +314,11 @@ __device__ void plan_serial(const PlanArgs& a, int* wave_tot, int* err_bits, int
   // Pass 1: chunk work before splitting (items and key tiles, head quads counted; the
   // largest block's tiles).
   __shared__ int max_blk_tiles;
-  if (threadIdx.x == 0) max_blk_tiles = 0;
+  if (hx::tid_x() == 0) max_blk_tiles = 0;
   __syncthreads();
   int64_t pf_items0 = 0, pf_tiles = 0;
   for (int b0 = 0; b0 < a.batch; b0 += kPlanThreads) {
-    const int b = b0 + (int)threadIdx.x;
+    const int b = b0 + hx::tid_x();
     int items = 0, tiles = 0, tmax = 0;
     if (b < a.batch) {
       int e = 0;
@@ -346,7 +346,7 @@ __device__ void plan_serial(const PlanArgs& a, int* wave_tot, int* err_bits, int
   auto chunk_wgs = [&](int st) -> int64_t {
     int64_t total = 0;
     for (int b0 = 0; b0 < a.batch; b0 += kPlanThreads) {
-      const int b = b0 + (int)threadIdx.x;
+      const int b = b0 + hx::tid_x();
       int wg = 0;
       if (b < a.batch) {
         int e = 0;
@@ -370,7 +370,7 @@ __device__ void plan_serial(const PlanArgs& a, int* wave_tot, int* err_bits, int
   // Pass 2: work lists.
   int base_dec = 0, base_pf = 0, base_comb = 0, base_slot = 0;
   for (int b0 = 0; b0 < a.batch; b0 += kPlanThreads) {
-    const int b = b0 + (int)threadIdx.x;
+    const int b = b0 + hx::tid_x();
     const bool active = b < a.batch;
     SeqMeta m{0, 0, 0, 0};
     if (active) m = plan_seq(a, b, err);
@@ -474,7 +474,7 @@ struct WaveTotals {
 
 // Block-wide exclusive scan of four counters at once; *total gets the block sums.
 __device__ int4 block_exclusive_scan4(int4 v, WaveTotals& wt, int& turn, int4* total) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int lane = hx::tid_x() & 63, w = hx::tid_x() >> 6, nw = hx::wg_size_x() >> 6;
   int4* t4 = wt.buf[turn];
   turn ^= 1;
   const int4 x = make_int4(wave_incl_scan<false>(v.x), wave_incl_scan<false>(v.y), wave_incl_scan<false>(v.z),
@@ -493,7 +493,7 @@ __device__ int4 block_exclusive_scan4(int4 v, WaveTotals& wt, int& turn, int4* t
 
 // Block-wide sum of v and max of m.
 __device__ int2 block_sum_max(int v, int m, WaveTotals& wt, int& turn) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int lane = hx::tid_x() & 63, w = hx::tid_x() >> 6, nw = hx::wg_size_x() >> 6;
   int4* t4 = wt.buf[turn];
   turn ^= 1;
   const int sv = __builtin_amdgcn_readlane(wave_incl_scan<false>(v), 63);
@@ -537,7 +537,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
   __shared__ int cs_off_p[kPlanChunkSeqs], cs_off_c[kPlanChunkSeqs], cs_off_s[kPlanChunkSeqs];
   // Flat block i: key tiles, then (after the split) its offsets within the flat order.
   __shared__ int fb_tiles[kPlanBlocks], fb_p[kPlanBlocks + 1], fb_c[kPlanBlocks + 1], fb_s[kPlanBlocks + 1];
-  const int tid = threadIdx.x;
+  const int tid = hx::tid_x();
   if (tid == 0) {  // published by the barrier of phase 0's scan
     err_bits = 0;
     best_st = INT32_MAX;
@@ -832,7 +832,7 @@ __device__ __forceinline__ Header read_header(const RunArgs& a) {
   r.counts = h0;
   r.ok = (h2.y == kPlanStamp) & (h1.x == a.batch) & (h1.y == a.max_q) & (h1.z == a.max_k) &
          (h1.w == a.hq) & (h2.x == a.hkv);
-  if (!r.ok && blockIdx.x == 0 && threadIdx.x == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_PLAN_MISMATCH);
+  if (!r.ok && hx::wg_x() == 0 && hx::tid_x() == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_PLAN_MISMATCH);
   return r;
 }
 
@@ -908,7 +908,7 @@ __device__ void append_rows(const RunArgs& a, int wg, int n_wg) {
   constexpr int kWords = kD / 8;  // 16-byte words per head row
   const int64_t per_token = (int64_t)a.hkv * kWords;
   const int64_t total = (int64_t)a.total_q * per_token;
-  for (int64_t idx = (int64_t)wg * kThreads + threadIdx.x; idx < total; idx += (int64_t)n_wg * kThreads) {
+  for (int64_t idx = (int64_t)wg * kThreads + hx::tid_x(); idx < total; idx += (int64_t)n_wg * kThreads) {
     const int64_t t = idx / per_token;
     const int rem = (int)(idx - t * per_token);
     const int h = rem / kWords, w = rem - h * kWords;
@@ -944,7 +944,7 @@ __global__ __launch_bounds__(kThreads, (decode_min_wgs<T, G>())) void decode_ker
   __shared__ float fin_m[8];
   __shared__ float fin_l[8];
 
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = hx::tid_x(), lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, held in a scalar register
   // XCD-aware order: workgroups go to the kXcds XCDs round-robin, so the hkv consecutive
   // workgroups an XCD receives are the KV heads of one split; each XCD then streams whole
@@ -952,12 +952,12 @@ __global__ __launch_bounds__(kThreads, (decode_min_wgs<T, G>())) void decode_ker
   // covers the work items rounded up to a multiple of kXcds.
   if constexpr (APPEND_ROWS) {
     const int dec_wgs = (a.grid_dec + kXcds - 1) / kXcds * kXcds * a.hkv;
-    if ((int)blockIdx.x >= dec_wgs) {  // append workgroups follow the decode workgroups
-      append_rows<T>(a, (int)blockIdx.x - dec_wgs, a.app_wgs);
+    if (hx::wg_x() >= dec_wgs) {  // append workgroups follow the decode workgroups
+      append_rows<T>(a, hx::wg_x() - dec_wgs, a.app_wgs);
       return;
     }
   }
-  const int xcd = (int)blockIdx.x % kXcds, jx = (int)blockIdx.x / kXcds;
+  const int xcd = hx::wg_x() % kXcds, jx = hx::wg_x() / kXcds;
   const int g = jx % a.hkv;
   const int item = (jx / a.hkv) * kXcds + xcd;
   if (item >= a.grid_dec) return;
@@ -967,7 +967,7 @@ __global__ __launch_bounds__(kThreads, (decode_min_wgs<T, G>())) void decode_ker
   const int4 it = a.dec_items[item];  // {b, split, q0, L}
   if (!hd.ok) return;
   const int n_dec = hd.counts.x;
-  if (blockIdx.x == 0 && tid == 0 && n_dec > a.grid_dec) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
+  if (hx::wg_x() == 0 && tid == 0 && n_dec > a.grid_dec) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
   if (item >= n_dec) return;
   // Workgroup-uniform: kept in scalar registers.
   const int b = __builtin_amdgcn_readfirstlane(it.x), s = __builtin_amdgcn_readfirstlane(it.y);
@@ -1279,13 +1279,13 @@ template <typename T, int G, int THREADS>
 __global__ __launch_bounds__(THREADS, 4) void combine_kernel(RunArgs a) {
   constexpr int kPerRow = G * (kD / 8);  // tasks per output row
   __shared__ float sh[10][THREADS];      // (m, l, acc[8]) of every range, one column per thread
-  const int cs = (int)blockIdx.x / a.hkv;
-  const int g = (int)blockIdx.x - cs * a.hkv;
+  const int cs = hx::wg_x() / a.hkv;
+  const int g = hx::wg_x() - cs * a.hkv;
   const Header hd = read_header(a);
   const int4 c = a.comb_seqs[cs];  // cs < grid_comb <= max_comb
   if (!hd.ok) return;
   const int n_comb = hd.counts.z;
-  if (blockIdx.x == 0 && threadIdx.x == 0 && n_comb > a.grid_comb) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
+  if (hx::wg_x() == 0 && hx::tid_x() == 0 && n_comb > a.grid_comb) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
   if (cs >= n_comb) return;
   const int first = c.y, splits = c.z & 0xffffff, rows = (c.z >> 24) + 1, q0 = c.w;
   if ((unsigned)c.x >= (unsigned)a.batch || first < 0 || splits < 1 || rows > kCombRows) return;
@@ -1294,7 +1294,7 @@ __global__ __launch_bounds__(THREADS, 4) void combine_kernel(RunArgs a) {
   const int tasks = rows * kPerRow;
   const int ranges = min(THREADS / tasks, splits);  // workgroup-uniform
   if (ranges <= 1) {
-    for (int t = threadIdx.x; t < tasks; t += THREADS) {
+    for (int t = hx::tid_x(); t < tasks; t += THREADS) {
       const int r = t / kPerRow;
       const int h = (t - r * kPerRow) >> 4, ch = t & 15;
       const CombAcc res = combine_range<T>(a, (int64_t)first + (int64_t)r * splits, g * G + h, ch, 0, splits);
@@ -1303,7 +1303,7 @@ __global__ __launch_bounds__(THREADS, 4) void combine_kernel(RunArgs a) {
     return;
   }
   // ranges >= 2: thread t < ranges * tasks takes task t % tasks over range t / tasks.
-  const int t = threadIdx.x;
+  const int t = hx::tid_x();
   const int task = t % tasks, rg = t / tasks;
   const int r = task / kPerRow;
   const int h = (task - r * kPerRow) >> 4, ch = task & 15;
@@ -1384,15 +1384,15 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   T* const vt_lds = reinterpret_cast<T*>(lds);                          // two V^T tiles
   T* const k_lds = reinterpret_cast<T*>(lds + 2 * 2 * kD * kVStride);    // two K tiles
 
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = hx::tid_x(), lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, held in a scalar register
-  const int item = (int)blockIdx.x / a.hkv;
-  const int g = (int)blockIdx.x - item * a.hkv;
+  const int item = hx::wg_x() / a.hkv;
+  const int g = hx::wg_x() - item * a.hkv;
   const Header hd = read_header(a);
   const int4 it = a.pf_items[item];  // item < grid_pf <= the list's capacity
   if (!hd.ok) return;
   const int n_pf = hd.counts.y;
-  if (blockIdx.x == 0 && tid == 0 && n_pf > a.grid_pf) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
+  if (hx::wg_x() == 0 && tid == 0 && n_pf > a.grid_pf) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
   if (item >= n_pf) return;
   // Work-item and sequence fields are workgroup-uniform: keep them (and the tile loop
   // they bound) in scalar registers.
@@ -1475,6 +1475,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   // same page; their scores are masked to -inf, so no branch guards the loads. A bad page
   // id reads page 0 and is reported in the error word.
   uint4 kreg[2], vreg[2];
+  bool bad_page = false;  // some tile's page id was outside the pool
   auto load_tile = [&](int t) {
     const int key_base = t * kTile;
     int64_t rowb;
@@ -1483,11 +1484,12 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
         pg_base = ld_pi;
         fetch_pages();
       }
+      // Wave-uniform: the page id, the row base and the bad-page flag stay in scalar
+      // registers (a branch around the error report here moved them to the VALU).
       int page = __builtin_amdgcn_readlane(pg_ids, ld_pi - pg_base);
-      if ((unsigned)page >= (unsigned)a.num_pages) {
-        if (tid == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_BAD_PAGE);
-        page = 0;
-      }
+      const bool bad = (unsigned)page >= (unsigned)a.num_pages;
+      bad_page |= bad;
+      page = bad ? 0 : page;
       rowb = (int64_t)page * a.page_size + ld_off;
       ld_off += kTile;
       if (ld_off == a.page_size) {
@@ -1565,7 +1567,8 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
     const bool full = __builtin_amdgcn_readfirstlane(full_i) != 0;
 
     v8 pb[2][2];
-    float alpha[2];
+    float mx[2];
+    bool move[2];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
       if (!full) {
@@ -1585,20 +1588,34 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
             if (16 * kb + i < rlo || 16 * kb + i > rhi) sacc[kb][rb][i] = -INFINITY;
       }
       // Row max on raw scores (the scale is positive), folded into exp2 by one FMA.
-      float mx = fmaxf(fmaxf(sacc[0][rb][0], sacc[0][rb][1]), fmaxf(sacc[0][rb][2], sacc[0][rb][3]));
+      float m = fmaxf(fmaxf(sacc[0][rb][0], sacc[0][rb][1]), fmaxf(sacc[0][rb][2], sacc[0][rb][3]));
 #pragma unroll
       for (int kb = 1; kb < 4; ++kb)
-        mx = fmaxf(mx, fmaxf(fmaxf(sacc[kb][rb][0], sacc[kb][rb][1]), fmaxf(sacc[kb][rb][2], sacc[kb][rb][3])));
-      mx = hx::max_xor32(hx::max_xor16(mx));
+        m = fmaxf(m, fmaxf(fmaxf(sacc[kb][rb][0], sacc[kb][rb][1]), fmaxf(sacc[kb][rb][2], sacc[kb][rb][3])));
+      mx[rb] = hx::max_xor32(hx::max_xor16(m));
       // Lazy max: the row's reference max moves only when the tile max exceeds it by more
       // than kLazyLog2 (log2 units). Until then p = 2^((s - m_run) * sl2) <= 2^kLazyLog2,
       // which the fp32 sums and bf16 P carry as accurately as p <= 1. With m_run = -inf
       // the test is mx > -inf (the first finite max sets it; alpha = 2^-inf = 0 then
       // multiplies the still-zero l and O); an all-masked tile (mx = -inf) never moves it.
-      const bool move = mx > m_run[rb] + lazy_thr;
-      alpha[rb] = move ? hx::fast_exp2((m_run[rb] - mx) * sl2) : 1.f;
-      const float m_new = move ? mx : m_run[rb];
-      const float neg_m = m_new != -INFINITY ? -m_new * sl2 : 0.f;
+      move[rb] = mx[rb] > m_run[rb] + lazy_thr;
+    }
+    // After a row's first tile its reference max rarely moves, so the factor alpha (two
+    // exps), the new max and the rescale of l and of the 64 accumulators run in a
+    // wave-uniform branch taken only when some row of the wave moved.
+    if (__any(move[0] || move[1])) {
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        const float alpha = move[rb] ? hx::fast_exp2((m_run[rb] - mx[rb]) * sl2) : 1.f;
+        m_run[rb] = move[rb] ? mx[rb] : m_run[rb];
+        l_run[rb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) oacc[db][rb] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const float neg_m = m_run[rb] != -INFINITY ? -m_run[rb] * sl2 : 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
@@ -1616,16 +1633,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
         psum = hx::dot8<T>(u, hx::ones8<T>(), psum);
         pb[ks][rb] = hx::as_v8<T>(u);
       }
-      l_run[rb] = l_run[rb] * alpha[rb] + psum;
-      m_run[rb] = m_new;
-    }
-    // Rescale the accumulators only when some row's reference max moved (rare after a
-    // row's first tile).
-    if (__any(alpha[0] != 1.f || alpha[1] != 1.f)) {
-#pragma unroll
-      for (int db = 0; db < 8; ++db)
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) oacc[db][rb] *= alpha[rb];
+      l_run[rb] += psum;
     }
 
     // O^T += V^T P^T with the key order of pb: {4(lane>>4)+0..3, 16+4(lane>>4)+0..3}.
@@ -1643,6 +1651,8 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
           oacc[db][rb] = E::mfma16x16x32(hx::as_v8<T>(vf[db]), pb[ks][rb], oacc[db][rb]);
     }
   }
+
+  if (bad_page && tid == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_BAD_PAGE);
 
   // Normalise: lane holds dims 16db+4(lane>>4)+0..3 of row 16rb+(lane&15). The rows go
   // through this wave's LDS staging area and leave as whole 256-byte head rows, four per
@@ -1736,9 +1746,9 @@ __global__ __launch_bounds__(256) void generic_kernel(RunArgs a, GenericShape gs
   __shared__ __attribute__((aligned(16))) float q_lds[kGenUnits * DMAX];
   __shared__ float p_lds[kGenUnits][kGenTile];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = hx::tid_x(), lane = tid & 63, w = tid >> 6;
   const int D = gs.head_dim;
-  int x = (int)blockIdx.x;
+  int x = hx::wg_x();
   const int hb = x % gs.head_blocks;
   x /= gs.head_blocks;
   const int g = x % a.hkv;

@@ -56,9 +56,9 @@ template <typename T>
 __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_append_kernel(RopeArgs a) {
   // One workgroup per packed row: the row's position, slot, RoPE factors and norm
   // weights are read once and reused by every head; wave w takes heads w, w + 4, ...
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t row = blockIdx.x;
+  const int lane = hx::tid_x() & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(hx::tid_x() >> 6);
+  const int64_t row = hx::wg_x();
   const int heads = a.hq + 2 * a.hkv;
   const int64_t slot = a.slots[row];
   const bool slot_ok = slot >= 0 && slot < a.pool_rows;
@@ -105,10 +105,10 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_append_kernel(RopeA
 // reduced over the 16 lanes of the head; the element arithmetic is the scalar kernel's.
 template <typename T>
 __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_append_vec_kernel(RopeArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = hx::tid_x() & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(hx::tid_x() >> 6);
   const int sub = lane >> 4, j = lane & 15;
-  const int64_t row = blockIdx.x;
+  const int64_t row = hx::wg_x();
   const int heads = a.hq + 2 * a.hkv;
   const int64_t slot = a.slots[row];
   const bool slot_ok = slot >= 0 && slot < a.pool_rows;

@@ -35,7 +35,7 @@ struct MetaArgs {
 // Each thread sums a contiguous run of ceil(n / 256) values; the 256 run totals are
 // scanned in LDS (Hillis-Steele); then each thread writes its run.
 __device__ void block_scan(const int32_t* in, int32_t* out, int n, int32_t* part) {
-  const int tid = threadIdx.x;
+  const int tid = hx::tid_x();
   const int per = (n + kMetaThreads - 1) / kMetaThreads;
   const int lo = min(n, tid * per), hi = min(n, lo + per);
   int32_t run = 0;
@@ -63,7 +63,7 @@ __global__ __launch_bounds__(kMetaThreads) void tick_meta_kernel(MetaArgs a) {
   __shared__ int32_t s_cuq[kMetaMaxBatch + 1];
   __shared__ int32_t s_aux[kMetaMaxBatch + 1];
   __shared__ int32_t s_part[kMetaThreads];
-  const int B = a.batch, tid = threadIdx.x;
+  const int B = a.batch, tid = hx::tid_x();
   for (int b = tid; b < B; b += kMetaThreads) {
     s_len[b] = a.seq[b];
     s_cnt[b] = a.seq[B + b];
@@ -71,7 +71,7 @@ __global__ __launch_bounds__(kMetaThreads) void tick_meta_kernel(MetaArgs a) {
   __syncthreads();
   block_scan(s_cnt, s_cuq, B, s_part);
 
-  if (blockIdx.x == 0) {
+  if (hx::wg_x() == 0) {
     for (int b = tid; b <= B; b += kMetaThreads) a.cu_q[b] = s_cuq[b];
     // Sequence ends E_b = length + count, their prefix sums, and seqused_k.
     for (int b = tid; b < B; b += kMetaThreads) {
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kMetaThreads) void tick_meta_kernel(MetaArgs a) {
   }
 
   // Token rows: row t belongs to the last sequence b with cu_q[b] <= t.
-  const int t = (int)(blockIdx.x - 1) * kMetaThreads + tid;
+  const int t = (int)(hx::wg_x() - 1) * kMetaThreads + tid;
   if (t >= a.total_q) return;
   int64_t pos = -1, slot = -1;
   if (t < s_cuq[B]) {
@@ -175,8 +175,8 @@ __global__ __launch_bounds__(256) void merge_kernel(uint16_t* out, int64_t o_row
                                                     int64_t n_rows, int hq) {
   // One wave per (entry j, head h); lane l owns dims l and l + 64. Every lane reads the old
   // lse before lane 0 stores the merged one, in program order within the wave.
-  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)hx::wg_x() * 4 + (hx::tid_x() >> 6);
+  const int lane = hx::tid_x() & 63;
   if (item >= n_rows * hq) return;
   const int64_t j = item / hq;
   const int h = (int)(item - j * hq);
