@@ -152,10 +152,18 @@ class DecodeBench:
         self.ops.kv_append(self.k_pools[layer], self.v_pools[layer], self.slots, self.k_new, self.v_new)
 
 
+GRAPH_WARM_S = 0.02   # replays before timing: the clocks ramp over the first milliseconds
+GRAPH_TIMED_S = 0.02  # the timed replays span at least this long
+
+
 def graph_time_us(calls, replays: int) -> float:
     """Mean device time of one call of ``calls`` (each launching one kernel), measured by
-    capturing them in one HIP graph and replaying it ``replays`` times between two
-    events on the current stream."""
+    capturing them in one HIP graph and replaying it between two events on the current
+    stream: ``replays`` times, or more so that the timed replays span GRAPH_TIMED_S,
+    after GRAPH_WARM_S of untimed replays (a short MFMA-bound launch measured cold runs
+    up to 15 % slower than in steady state)."""
+    import math
+
     import torch
 
     for call in calls:   # warm (first launches, allocator) outside the graph
@@ -165,8 +173,13 @@ def graph_time_us(calls, replays: int) -> float:
     with torch.cuda.graph(graph):
         for call in calls:
             call()
+    t0 = time.perf_counter()
     graph.replay()
     torch.cuda.synchronize()
+    once = max(time.perf_counter() - t0, 1e-6)
+    for _ in range(math.ceil(GRAPH_WARM_S / once)):
+        graph.replay()
+    replays = max(replays, math.ceil(GRAPH_TIMED_S / once))
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(replays):
