@@ -1,13 +1,19 @@
-"""Split decode rows over repeated runs of one plan.
+"""Split decode rows and split chunk blocks over repeated runs of one plan.
 
-A decode row longer than 256 keys is split over several workgroups. Each writes a
-partial (o / l, max, sum) to the plan's workspace, and the combine kernel merges the
-row's partials in split order. Every run of the plan reuses the same partial slots.
+A decode row longer than 256 keys is split over several workgroups, and so is a chunk
+row block whose key tiles are split. Each split writes a partial (o / l, max, sum) to the
+plan's workspace, and the combine kernel merges each row's partials in split order.
+Every run of the plan reuses the same partial slots.
 
-One plan is run many times, alternating V and -V in the pool. Negating V keeps every
-softmax weight and negates every product, so the output of a -V run is the exact
-negation of a V run's output. The checks:
-- every V run gives the bits of the first, and every -V run their negation;
+One plan is run many times, alternating V and c * V in the pool. Scaling V keeps every
+softmax weight and scales every product, so the output of a c * V run is exactly c times
+a V run's output, for c = -1 on decode rows (fp32 VALU arithmetic, odd in V) and c = 2
+where chunk rows run on MFMA: the MFMA accumulation is not odd in V (the committed C4
+chunk output differs from its -V negation by about an ulp in 55 of 4104 rows), while a
+power-of-two scale commutes with every rounding in bf16 (in fp16, outputs this small are
+subnormal and do not scale exactly, so the chunk cases run in bf16; fp16 split partials
+are checked against the oracle in test_gpu_attn.py). The checks:
+- every V run gives the bits of the first, and every c * V run c times them;
 - a partial left over from the previous run (a slot not rewritten, or read before it
   was) would mix signs or values in some row;
 - the first run is checked against the float64 oracle on sampled rows.
@@ -41,36 +47,59 @@ def _decoders(seed: int, hq: int, hkv: int, batch: int, lo: int, hi: int) -> syn
                           n_q_heads=hq, n_kv_heads=hkv, seed=seed)
 
 
+def _mixed(seed: int, decoders: int, chunk: int, cached: int) -> synth.Workload:
+    """Decode rows of 1000-3000 keys plus one chunk of ``chunk`` rows after ``cached``
+    cached keys, whose row blocks the plan splits over key tiles."""
+    rng = np.random.default_rng(seed)
+    done = [int(x) for x in rng.integers(1000, 3001, decoders)] + [cached]
+    q_lens = [1] * decoders + [chunk]
+    pages = [-(-(c + n) // 256) for c, n in zip(done, q_lens)]
+    perm = [int(p) for p in rng.permutation(sum(pages) + 8)]
+    tables, i = [], 0
+    for n in pages:
+        tables.append(perm[i:i + n])
+        i += n
+    return synth.Workload("mixed split chunk", q_lens, done, tables, sum(pages) + 8, seed=seed)
+
+
+# name: (workload, dtype, window, scale c of the alternate runs)
 CASES = {
-    "c2 bf16": (synth.c2, torch.bfloat16, (-1, 0)),
-    "c2 fp16, window 1000": (synth.c2, torch.float16, (1000, 0)),
-    "G=8 bf16": (lambda: _decoders(31, 64, 8, 24, 300, 9000), torch.bfloat16, (-1, 0)),
-    "G=1 bf16": (lambda: _decoders(32, 8, 8, 40, 300, 5000), torch.bfloat16, (-1, 0)),
-    "G=2 fp16": (lambda: _decoders(33, 16, 8, 40, 300, 5000), torch.float16, (-1, 0)),
+    "c2 bf16": (synth.c2, torch.bfloat16, (-1, 0), -1.0),
+    "c2 fp16, window 1000": (synth.c2, torch.float16, (1000, 0), -1.0),
+    "G=8 bf16": (lambda: _decoders(31, 64, 8, 24, 300, 9000), torch.bfloat16, (-1, 0), -1.0),
+    "G=1 bf16": (lambda: _decoders(32, 8, 8, 40, 300, 5000), torch.bfloat16, (-1, 0), -1.0),
+    "G=2 fp16": (lambda: _decoders(33, 16, 8, 40, 300, 5000), torch.float16, (-1, 0), -1.0),
+    "c3 bf16 (split chunk blocks)": (synth.c3, torch.bfloat16, (-1, 0), 2.0),
+    "1024-row chunk after 4096 keys": (lambda: _mixed(34, 8, 1024, 4096), torch.bfloat16, (-1, 0), 2.0),
 }
 
 
 @pytest.mark.parametrize("name", list(CASES))
 def test_repeated_runs_merge_split_rows_exactly(device, name):
-    make, dtype, window = CASES[name]
+    make, dtype, window, scale = CASES[name]
     w = make()
     say(f"split merge {name}: batch={w.batch} max_k={w.max_k} runs={RUNS}")
     tick = DeviceTick(w, dtype, device, pool_on_device=True)
     plan = tick.plan(window=window)
-    v_neg = -tick.v_pool
+    v_alt = tick.v_pool * scale
     first = plan.run(tick.q, tick.k_pool, tick.v_pool, tick.block_table)
     torch.cuda.synchronize()
     assert plan.error_word() == 0
     sample = list(range(0, w.batch, max(1, w.batch // 12)))
-    ref, _ = tick.oracle(window=window, rows={b: [0] for b in sample})
-    compare(first, ref, what=f"split merge {name}", rows=np.array(sample))
+    rows = {b: [0] for b in sample}
+    for b, n in enumerate(w.q_lens):  # chunk rows: the first, middle and last of each
+        if n > 1:
+            rows[b] = sorted({0, 63, 64, n // 2, n - 1})
+    ref, _ = tick.oracle(window=window, rows=rows)
+    flat = [w.cu_seq_q[b] + r for b, rs in sorted(rows.items()) for r in rs]
+    compare(first, ref, what=f"split merge {name}", rows=np.array(flat))
     # Compared as values (an output that cancels to +0 stays +0 under -V); every other
     # value must match bit for bit.
-    want_neg = -first
+    want_alt = first * scale
     out = torch.empty_like(first)
     for i in range(RUNS):
-        neg = i % 2 == 0
-        plan.run(tick.q, tick.k_pool, v_neg if neg else tick.v_pool, tick.block_table, out=out)
-        bad = (out != (want_neg if neg else first)).any(dim=2).any(dim=1)
+        alt = i % 2 == 0
+        plan.run(tick.q, tick.k_pool, v_alt if alt else tick.v_pool, tick.block_table, out=out)
+        bad = (out != (want_alt if alt else first)).any(dim=2).any(dim=1)
         assert not bool(bad.any()), (name, i, "rows differ", torch.nonzero(bad).flatten()[:8].tolist())
     assert plan.error_word() == 0
