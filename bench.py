@@ -152,41 +152,58 @@ class DecodeBench:
         self.ops.kv_append(self.k_pools[layer], self.v_pools[layer], self.slots, self.k_new, self.v_new)
 
 
-GRAPH_WARM_S = 0.02   # replays before timing: the clocks ramp over the first milliseconds
-GRAPH_TIMED_S = 0.02  # the timed replays span at least this long
+GRAPH_WARM_S = 0.02     # replays before timing: the clocks ramp over the first milliseconds
+GRAPH_TIMED_S = 0.02    # the timed replays span at least this long
+GRAPH_REPLAY_S = 4e-4   # one replay holds enough launches to hide the host's replay cost
 
 
 def graph_time_us(calls, replays: int) -> float:
     """Mean device time of one call of ``calls`` (each launching one kernel), measured by
     capturing them in one HIP graph and replaying it between two events on the current
-    stream: ``replays`` times, or more so that the timed replays span GRAPH_TIMED_S,
-    after GRAPH_WARM_S of untimed replays (a short MFMA-bound launch measured cold runs
-    up to 15 % slower than in steady state)."""
+    stream.
+
+    - The graph holds ``calls`` repeated so that one replay lasts about GRAPH_REPLAY_S: a
+      replay costs the host about 17 us, which a single short launch (a 64-row append,
+      a combine) would otherwise measure instead of itself.
+    - It is replayed ``replays`` times, or more so that the timed replays span
+      GRAPH_TIMED_S, after GRAPH_WARM_S of untimed replays (a short MFMA-bound launch
+      measured cold runs up to 15 % slower than in steady state)."""
     import math
 
     import torch
 
+    def capture(repeat: int):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(repeat):
+                for call in calls:
+                    call()
+        return graph
+
+    def replay_s(graph, n: int) -> float:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(n):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1e-3 / n
+
     for call in calls:   # warm (first launches, allocator) outside the graph
         call()
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for call in calls:
-            call()
-    t0 = time.perf_counter()
-    graph.replay()
+    probe = capture(1)
+    probe.replay()
     torch.cuda.synchronize()
-    once = max(time.perf_counter() - t0, 1e-6)
+    device_s = replay_s(probe, 20)  # an upper bound on the calls' device time
+    del probe
+    repeat = max(1, min(64, math.ceil(GRAPH_REPLAY_S / device_s)))
+    graph = capture(repeat)
+    once = max(replay_s(graph, 1), 1e-6)
     for _ in range(math.ceil(GRAPH_WARM_S / once)):
         graph.replay()
     replays = max(replays, math.ceil(GRAPH_TIMED_S / once))
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(replays):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    us = start.elapsed_time(end) * 1e3 / (replays * len(calls))
+    us = replay_s(graph, replays) * 1e6 / (repeat * len(calls))
     del graph
     return us
 

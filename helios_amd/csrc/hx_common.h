@@ -8,16 +8,17 @@
 
 namespace hx {
 
-// Work-item and workgroup indices and sizes along x, read with the intrinsics. HIP's
-// threadIdx / blockIdx / blockDim / gridDim go through device-library functions built for
-// IEEE mode, which the inliner keeps out of these non-IEEE kernels: every use was a real
-// call, and a kernel that calls gives up registers to the calling convention.
+// Work-item and workgroup indices and the workgroup size along x, read with the
+// intrinsics. HIP's threadIdx / blockIdx / blockDim / gridDim go through device-library
+// functions built for IEEE mode, which the inliner keeps out of these non-IEEE kernels:
+// every use was a real call, and a kernel that calls gives up registers to the calling
+// convention. The workgroup count is not read on the device: the grid size intrinsic
+// loads it from the dispatch packet in the queue's host-visible memory, an uncached read
+// per workgroup that made a 2048-row append 4x slower; grid-stride kernels take their
+// workgroup count as an argument instead.
 __device__ __forceinline__ int tid_x() { return (int)__builtin_amdgcn_workitem_id_x(); }
 __device__ __forceinline__ int wg_x() { return (int)__builtin_amdgcn_workgroup_id_x(); }
 __device__ __forceinline__ int wg_size_x() { return (int)__builtin_amdgcn_workgroup_size_x(); }
-__device__ __forceinline__ int num_wg_x() {
-  return (int)(__builtin_amdgcn_grid_size_x() / __builtin_amdgcn_workgroup_size_x());
-}
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));

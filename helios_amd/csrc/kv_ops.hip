@@ -23,6 +23,7 @@ struct AppendArgs {
   int32_t n_kv;
   int32_t head_b;   // bytes of one head row (head_dim * elem_bytes)
   int32_t words;    // words of type W per head row
+  int32_t n_wg;     // workgroups of the launch (the grid stride is n_wg * 256 threads)
 };
 
 template <typename W>
@@ -30,8 +31,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   const int64_t per_token = (int64_t)a.n_kv * a.words;
   const int64_t total = a.n_tokens * per_token;
   const int64_t pool_row_b = (int64_t)a.n_kv * a.head_b;
-  for (int64_t idx = (int64_t)hx::wg_x() * hx::wg_size_x() + hx::tid_x(); idx < total;
-       idx += (int64_t)hx::num_wg_x() * hx::wg_size_x()) {
+  for (int64_t idx = (int64_t)hx::wg_x() * 256 + hx::tid_x(); idx < total; idx += (int64_t)a.n_wg * 256) {
     const int64_t t = idx / per_token;
     const int rem = (int)(idx - t * per_token);
     const int h = rem / a.words;
@@ -75,6 +75,7 @@ struct CopyArgs {
   int32_t n_tensors;
   int32_t n_pages;
   int32_t tiles_per_page;
+  int32_t n_wg;  // workgroups of the launch (the grid stride in tiles)
 };
 
 // Grid-stride over 16 KiB tiles of (tensor, page pair): each thread streams four
@@ -83,7 +84,7 @@ struct CopyArgs {
 // (the first form of this kernel) reached only ~2.6 TB/s.
 __global__ __launch_bounds__(kCopyThreads) void kv_copy_pages_kernel(CopyArgs a) {
   const int64_t total = (int64_t)a.n_tensors * a.n_pages * a.tiles_per_page;
-  for (int64_t t = hx::wg_x(); t < total; t += hx::num_wg_x()) {
+  for (int64_t t = hx::wg_x(); t < total; t += a.n_wg) {
     const int tile = (int)(t % a.tiles_per_page);
     const int64_t rest = t / a.tiles_per_page;
     const int pair = (int)(rest % a.n_pages);
@@ -120,14 +121,14 @@ struct GatherArgs {
   int32_t n_kv;
   int32_t head_b;
   int32_t words;
+  int32_t n_wg;  // workgroups of the element-wise launch (its grid stride is n_wg * 256)
 };
 
 template <typename W>
 __global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
   const int64_t per_head = a.length * a.words;
   const int64_t total = (int64_t)a.n_kv * per_head;
-  for (int64_t idx = (int64_t)hx::wg_x() * hx::wg_size_x() + hx::tid_x(); idx < total;
-       idx += (int64_t)hx::num_wg_x() * hx::wg_size_x()) {
+  for (int64_t idx = (int64_t)hx::wg_x() * 256 + hx::tid_x(); idx < total; idx += (int64_t)a.n_wg * 256) {
     const int h = (int)(idx / per_head);
     const int64_t rem = idx - (int64_t)h * per_head;
     const int64_t j = rem / a.words;
@@ -234,6 +235,7 @@ int hx_kv_append(void* k_pool, void* v_pool, int64_t pool_rows,
                                  (uint64_t)(uintptr_t)k_new, (uint64_t)(uintptr_t)v_new});
   a.words = a.head_b / wb;
   const int grid = grid_for(n_tokens * n_kv_heads * (int64_t)a.words, 256);
+  a.n_wg = grid;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (wb) {
     case 16: hipLaunchKernelGGL(kv_append_kernel<uint4>, dim3(grid), dim3(256), 0, s, a); break;
@@ -289,6 +291,7 @@ int hx_kv_copy_pages(void* const* k_pools, void* const* v_pools, int32_t n_layer
       a.tiles_per_page = tiles;
       int64_t grid = (int64_t)nt * np * tiles;
       if (grid > kCopyMaxGrid) grid = kCopyMaxGrid;
+      a.n_wg = (int32_t)grid;
       hipLaunchKernelGGL(kv_copy_pages_kernel, dim3((unsigned)grid), dim3(kCopyThreads), 0, s, a);
       const hipError_t e = hipGetLastError();
       if (e != hipSuccess) return (int)e;
@@ -335,6 +338,7 @@ int hx_kv_gather(const void* pool, int32_t num_pool_pages, int32_t page_size,
     if (launched) return hx::status_from_hip(hipGetLastError());
   }
   const int grid = grid_for((int64_t)n_kv_heads * length * a.words, 256);
+  a.n_wg = grid;
   switch (wb) {
     case 16: hipLaunchKernelGGL(kv_gather_kernel<uint4>, dim3(grid), dim3(256), 0, s, a); break;
     case 8: hipLaunchKernelGGL(kv_gather_kernel<uint2>, dim3(grid), dim3(256), 0, s, a); break;
