@@ -514,15 +514,18 @@ __device__ int2 block_sum_max(int v, int m, WaveTotals& wt, int& turn) {
 // and blocks are split over their key tiles; see chunk_split_tiles / refine_split_tiles).
 //
 // The row blocks of all chunks are listed in LDS once (kPlanBlocks at most, over at most
-// kPlanChunkSeqs chunk sequences), in the order their items are emitted: sequences in
-// order, each sequence's blocks from the last to the first (later blocks see more keys
-// under a causal mask, so they start first). Every pass over them runs on all threads:
-// the split-size search sums split counts over the list, and a scan over the list gives
-// each block its item, partial-slot and combine-record offsets. Larger ticks take the
-// serial walk (plan_serial), which produces the same lists.
+// kPlanChunkSeqs chunk sequences) in flat order: sequences in order, each sequence's
+// blocks from the last to the first (later blocks see more keys under a causal mask).
+// Every pass over them runs on all threads: the split-size search sums split counts over
+// the list, and a scan over the list gives each block its partial-slot and
+// combine-record offsets. Chunk items follow the flat order, except that a tick of at
+// most kPlanSortBlocks blocks lists them longest first (see phase 5). Larger ticks take
+// the serial walk (plan_serial), which produces the same lists.
 constexpr int kPlanChunkSeqs = 1024;
 constexpr int kPlanBlocks = 4096;
 constexpr int kPlanSearchWork = 1 << 16;  // candidates x blocks evaluated in one pass
+constexpr int kPlanSortBlocks = 256;
+static_assert(2 * kPlanSortBlocks <= kPlanThreads, "sort keys and item counts share the search buffer");
 
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
   __shared__ int wave_tot[kPlanThreads / 64];
@@ -740,7 +743,23 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
 
   // Phase 5: chunk items, their first partial rows, and combine records, one block per
   // thread. A split block's rows own S consecutive partial slots each; its combine
-  // records cover kCombRows rows each.
+  // records cover kCombRows rows each. A block's items stay together (head quads, then
+  // splits). With at most kPlanSortBlocks blocks the blocks go longest first: by key
+  // tiles per item, descending, ties in flat order. Workgroups start in index order as
+  // CUs free up, so the short items fill the last round instead of the long ones
+  // (greedy longest-first scheduling); on a tick of two chunks of 1024 and 992 rows the
+  // chunk kernel's 512 split workgroups otherwise end with a sequence's long blocks.
+  const bool by_length = n_blk > 0 && n_blk <= kPlanSortBlocks;
+  int* const blk_key = cand_wgs;                      // free after the split search
+  int* const blk_items = cand_wgs + kPlanSortBlocks;
+  if (by_length) {
+    if (tid < n_blk) {
+      const int S = chunk_split_count(fb_tiles[tid], split_tiles);
+      blk_key[tid] = (fb_tiles[tid] + S - 1) / S;
+      blk_items[tid] = S * a.head_quads;
+    }
+    __syncthreads();
+  }
   for (int i = tid; i < n_blk; i += kPlanThreads) {
     int k, blk;
     block_of(i, k, blk);
@@ -749,7 +768,15 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
     const int row0 = blk * a.rows_per_item;
     const int S = chunk_split_count(fb_tiles[i], split_tiles);
     const int rows = min(a.rows_per_item, n - row0);
-    const int item0 = cs_off_p[k] + fb_p[i] - fb_p[f0];
+    int item0 = cs_off_p[k] + fb_p[i] - fb_p[f0];
+    if (by_length) {
+      const int key = blk_key[i];
+      item0 = 0;
+      for (int j = 0; j < n_blk; ++j) {
+        const int kj = blk_key[j];
+        item0 += kj > key || (kj == key && j < i) ? blk_items[j] : 0;
+      }
+    }
     const int slot = cs_off_s[k] + fb_s[i] - fb_s[f0];
     const int comb0 = cs_off_c[k] + fb_c[i] - fb_c[f0];
     const bool fits = S == 1 || slot + rows * S <= a.cslot_cap;

@@ -10,7 +10,9 @@ workspace. This module builds the same lists from the host lengths:
 - combine records {b, first slot, splits | (rows - 1) << 24, first output row}: one per
   multi-split decode row, and one per 8 rows of a split chunk block.
 
-Sequences go in order and a chunk's row blocks from the last to the first. The split size
+Sequences go in order and a chunk's row blocks from the last to the first. When the tick
+has at most 256 row blocks, the chunk items are then reordered block by block, longest
+first: by key tiles per item, descending, ties in that order. The split size
 follows the documented rule (at least max(8, ceil(tiles * Hkv / 512)) tiles when the
 unsplit chunk items launch fewer than 512 workgroups, raised to the smallest size that
 fits whole rounds of 256 workgroups). The workspace offsets mirror make_layout.
@@ -27,6 +29,7 @@ CUS = 256
 MIN_SPLIT_TILES = 8
 MAX_SPLITS = 64
 COMB_ROWS = 8
+SORT_BLOCKS = 256  # ticks of at most this many row blocks list chunk items longest first
 HEADER_WORDS = 64
 HEAD_DIM = 128
 
@@ -113,7 +116,8 @@ def plan_lists(q_lens, k_lens, hq: int, hkv: int, window, max_dec: int, cslot_ca
     arrays, in the planner's order."""
     rpi, quads = geometry(hq, hkv)
     st = split_tiles(q_lens, k_lens, hq, hkv, window)
-    seq, dec, pf, pfb, comb = [], [], [], [], []
+    seq, dec, comb = [], [], []
+    blocks = []  # flat order: (tiles per item, chunk items, their partial bases)
     q0 = 0
     slot = 0
     for b, (n, L) in enumerate(zip(q_lens, k_lens)):
@@ -131,15 +135,18 @@ def plan_lists(q_lens, k_lens, hq: int, hkv: int, window, max_dec: int, cslot_ca
                 S = split_count(chunk_tiles(n, L, row0, rpi, window), st)
                 rows = min(rpi, n - row0)
                 assert S == 1 or slot + rows * S <= cslot_cap, "model cases must fit the slots"
-                for hq_i in range(quads):
-                    for sp in range(S):
-                        pf.append((b, row0, hq_i, sp | ((S - 1) << 16)))
-                        pfb.append(slot)
+                tiles = chunk_tiles(n, L, row0, rpi, window)
+                items = [(b, row0, hq_i, sp | ((S - 1) << 16)) for hq_i in range(quads) for sp in range(S)]
+                blocks.append((_ceil(tiles, S), items, [slot] * len(items)))
                 if S > 1:
                     for r in range(0, rows, COMB_ROWS):
                         nr = min(COMB_ROWS, rows - r)
                         comb.append((b, max_dec + slot + r * S, S | ((nr - 1) << 24), q0 + row0 + r))
                     slot += rows * S
         q0 += n
+    if len(blocks) <= SORT_BLOCKS:
+        blocks.sort(key=lambda blk: -blk[0])  # stable: ties keep the flat order
+    pf = [it for blk in blocks for it in blk[1]]
+    pfb = [base for blk in blocks for base in blk[2]]
     as_arr = lambda x, w: np.array(x, dtype=np.int64).reshape(-1, w).astype(np.int32)  # noqa: E731
     return as_arr(seq, 4), as_arr(dec, 4), as_arr(pf, 4), np.array(pfb, dtype=np.int32), as_arr(comb, 4)
