@@ -299,8 +299,10 @@ def cpu_tick_baseline(w, *, rows_kept: dict[int, int] | None = None, seconds_bud
             "gflops": round(flops / sec / 1e9, 2), "cores": cores, "reps": len(times)}
 
 
-def packed_tick(device, steps: int = 30, warmup: int = 5):
-    """One layer of the mixed tick: append + decode/chunk attention, wall time."""
+def packed_tick(device, steps: int = 200, warmup: int = 200):
+    """One layer of the mixed tick: append + decode/chunk attention, wall time. About
+    25 ms of warm-up steps go first: after the pools are filled the clocks take a few
+    milliseconds to settle (5 warm-up steps and 30 timed ones read about 10 % high)."""
     import torch
 
     from helios_amd import synth
