@@ -15,7 +15,8 @@ has at most 256 row blocks, the chunk items are then reordered block by block, l
 first: by key tiles per item, descending, ties in that order. The split size
 follows the documented rule (at least max(8, ceil(tiles * Hkv / 512)) tiles when the
 unsplit chunk items launch fewer than 512 workgroups, raised to the smallest size that
-fits whole rounds of 256 workgroups). The workspace offsets mirror make_layout.
+fits whole rounds of 256 workgroups); then only blocks longer than max(split size,
+1.25 x the chunk tiles per CU) split. The workspace offsets mirror make_layout.
 """
 
 from __future__ import annotations
@@ -53,8 +54,17 @@ def chunk_tiles(n: int, L: int, row0: int, rows_per_item: int, window: tuple[int
     return (khi // TILE + 1 - klo // TILE) if khi >= klo else 0
 
 
-def split_count(tiles: int, st: int) -> int:
-    return 1 if st <= 0 or tiles <= st else min(MAX_SPLITS, _ceil(tiles, st))
+def split_count(tiles: int, st: int, keep: int | None = None) -> int:
+    keep = st if keep is None else keep
+    return 1 if st <= 0 or tiles <= keep else min(MAX_SPLITS, _ceil(tiles, st))
+
+
+def keep_tiles(q_lens, k_lens, hq: int, hkv: int, window, st: int) -> int:
+    """Blocks of at most this many tiles stay whole: 1.25 x the chunk tiles per CU."""
+    rpi, quads = geometry(hq, hkv)
+    tiles = quads * sum(chunk_tiles(n, L, r0, rpi, window)
+                        for n, L in zip(q_lens, k_lens) if n >= 2 for r0 in range(0, n, rpi))
+    return max(st, _ceil(5 * tiles * hkv, 4 * CUS))
 
 
 def split_tiles(q_lens, k_lens, hq: int, hkv: int, window) -> int:
@@ -116,6 +126,7 @@ def plan_lists(q_lens, k_lens, hq: int, hkv: int, window, max_dec: int, cslot_ca
     arrays, in the planner's order."""
     rpi, quads = geometry(hq, hkv)
     st = split_tiles(q_lens, k_lens, hq, hkv, window)
+    keep = keep_tiles(q_lens, k_lens, hq, hkv, window, st)
     seq, dec, comb = [], [], []
     blocks = []  # flat order: (tiles per item, chunk items, their partial bases)
     q0 = 0
@@ -132,7 +143,7 @@ def plan_lists(q_lens, k_lens, hq: int, hkv: int, window, max_dec: int, cslot_ca
         elif n >= 2:
             for blk in reversed(range(_ceil(n, rpi))):
                 row0 = blk * rpi
-                S = split_count(chunk_tiles(n, L, row0, rpi, window), st)
+                S = split_count(chunk_tiles(n, L, row0, rpi, window), st, keep)
                 rows = min(rpi, n - row0)
                 assert S == 1 or slot + rows * S <= cslot_cap, "model cases must fit the slots"
                 tiles = chunk_tiles(n, L, row0, rpi, window)

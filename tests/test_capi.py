@@ -61,7 +61,8 @@ def _expected_counts(w: synth.Workload, window=(-1, 0)):
     each block's 64-key tiles are cut into splits of at least max(8, ceil(tiles * Hkv /
     512)) tiles, every split row adding one combine record. When the split workgroups
     spill past R >= 1 whole rounds of 256 (one chunk workgroup per CU), the split size is
-    the smallest one, up to the largest block's tiles, whose count fits R rounds."""
+    the smallest one, up to the largest block's tiles, whose count fits R rounds. Then
+    only blocks longer than max(split size, ceil(1.25 x chunk tiles x Hkv / 256)) split."""
     nd = nc = npf = 0
     G = w.n_q_heads // w.n_kv_heads
     gw = min(G, 4)
@@ -82,8 +83,9 @@ def _expected_counts(w: synth.Workload, window=(-1, 0)):
     if items0 and items0 * w.n_kv_heads < 512:
         split = max(8, -(-tiles0 * w.n_kv_heads // 512))
 
-    def split_count(t, st):
-        return 1 if not st or t <= st else min(64, -(-t // st))
+    def split_count(t, st, keep=None):
+        keep = st if keep is None else keep
+        return 1 if not st or t <= keep else min(64, -(-t // st))
 
     def wgs(st):
         return w.n_kv_heads * quads * sum(split_count(tiles(*blk), st) for blk in blocks)
@@ -93,6 +95,7 @@ def _expected_counts(w: synth.Workload, window=(-1, 0)):
         rounds, max_t = w0 // 256, max(tiles(*blk) for blk in blocks)
         if rounds >= 1 and w0 % 256 and max_t > split and wgs(max_t) <= rounds * 256:
             split = min(st for st in range(split, max_t + 1) if wgs(st) <= rounds * 256)
+    keep = max(split, -(-5 * tiles0 * w.n_kv_heads // (4 * 256)))
     for n, L in zip(w.q_lens, w.k_lens):
         if n == 1:
             lo = 0 if window[0] < 0 else max(0, L - 1 - window[0])
@@ -101,7 +104,7 @@ def _expected_counts(w: synth.Workload, window=(-1, 0)):
             nc += splits > 1
     for n, L, r0 in blocks:
         t = tiles(n, L, r0)
-        s = split_count(t, split)
+        s = split_count(t, split, keep)
         npf += s * quads
         if s > 1:
             nc += -(-min(rows_per_item, n - r0) // 8)  # combine records of up to 8 rows
