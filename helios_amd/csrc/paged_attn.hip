@@ -179,21 +179,42 @@ __host__ __device__ inline int chunk_keep_tiles(int64_t tiles, int hkv, int spli
 // spills past R >= 1 whole rounds, returns the smallest st whose count fits R rounds,
 // if one does; otherwise st0. The plan kernel and the host count call it with the same
 // counts, so both reach the same split size.
+// Smallest split size in (lo, hi] whose workgroups fit `target`, given wgs(lo) > target;
+// 0 when even hi does not fit.
 template <typename WgsFn>
-__host__ __device__ inline int refine_split_tiles(int st0, int max_tiles, WgsFn wgs) {
-  if (st0 <= 0 || max_tiles <= st0) return st0;
-  const int64_t w0 = wgs(st0);
-  const int64_t rounds = w0 / kChunkCUs;
-  if (rounds < 1 || w0 % kChunkCUs == 0) return st0;
-  const int64_t target = rounds * kChunkCUs;
-  int lo = st0, hi = max_tiles;  // wgs(lo) > target
-  if (wgs(hi) > target) return st0;
+__host__ __device__ inline int smallest_fitting_split(int lo, int hi, int64_t target, WgsFn wgs) {
+  if (wgs(hi) > target) return 0;
   while (hi - lo > 1) {
     const int mid = lo + (hi - lo) / 2;
     if (wgs(mid) <= target) hi = mid;
     else lo = mid;
   }
   return hi;
+}
+
+// One round instead of several: when the smallest split size whose workgroups fit one
+// round of kChunkCUs is at most one_round_tiles (1.25 x the chunk tiles per CU,
+// chunk_keep_tiles), the pieces are no longer than the blocks the planner keeps whole,
+// so one round of them ends about when the longest item would anyway, without a second
+// round's fixed costs and with fewer partial rows. Blocks of a chunk far into its
+// sequence have nearly equal tile counts: a 1024-row chunk at position 4096 (blocks of
+// 65-80 tiles) takes 40-tile splits in 256 workgroups instead of 21-tile splits in 512
+// (chunk 88.8 -> 88.1 us, combine 12.8 -> 10.6 us).
+template <typename WgsFn>
+__host__ __device__ inline int refine_split_tiles(int st0, int max_tiles, int one_round_tiles, WgsFn wgs) {
+  if (st0 <= 0 || max_tiles <= st0) return st0;
+  int st = st0;
+  const int64_t w0 = wgs(st0);
+  const int64_t rounds = w0 / kChunkCUs;
+  if (rounds >= 1 && w0 % kChunkCUs != 0) {
+    const int s = smallest_fitting_split(st0, max_tiles, rounds * kChunkCUs, wgs);
+    if (s > 0) st = s;
+  }
+  if (w0 > kChunkCUs) {
+    const int s1 = smallest_fitting_split(st0, max_tiles, kChunkCUs, wgs);
+    if (s1 > 0 && s1 <= one_round_tiles) st = s1;
+  }
+  return st;
 }
 
 // Decode key window of a one-token row at position L-1: keys [lo, L).
@@ -382,7 +403,8 @@ __device__ void plan_serial(const PlanArgs& a, int* wave_tot, int* err_bits, int
     }
     return total * a.hkv;
   };
-  const int split_tiles = refine_split_tiles(chunk_split_tiles(pf_tiles, pf_items0, a.hkv), max_blk_tiles, chunk_wgs);
+  const int split_tiles = refine_split_tiles(chunk_split_tiles(pf_tiles, pf_items0, a.hkv), max_blk_tiles,
+                                             chunk_keep_tiles(pf_tiles, a.hkv, 0), chunk_wgs);
   const int keep_tiles = chunk_keep_tiles(pf_tiles, a.hkv, split_tiles);
 
   // Pass 2: work lists.
@@ -550,7 +572,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
   __shared__ WaveTotals wt;
   __shared__ int err_bits;
   __shared__ int cand_wgs[kPlanThreads];  // split-size search: workgroups per candidate
-  __shared__ int best_st;
+  __shared__ int best_st, best_one;
   // Chunk sequence k: its sequence index, first row, clamped (n, L), first flat block, and its item /
   // combine-record / partial-slot offsets once known.
   __shared__ int cs_b[kPlanChunkSeqs], cs_q0[kPlanChunkSeqs], cs_n[kPlanChunkSeqs], cs_L[kPlanChunkSeqs];
@@ -562,6 +584,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
   if (tid == 0) {  // published by the barrier of phase 0's scan
     err_bits = 0;
     best_st = INT32_MAX;
+    best_one = INT32_MAX;
   }
   int err = 0;
   int turn = 0;  // WaveTotals buffer of the next block-wide scan
@@ -665,8 +688,15 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
         __syncthreads();
         if (best_st != INT32_MAX) split_tiles = best_st;
       }
+      // One round instead, as refine_split_tiles.
+      if (w0 > kChunkCUs) {
+        if (tid >= 1 && tid <= ncand && (int64_t)cand_wgs[tid] * a.head_quads * a.hkv <= kChunkCUs)
+          atomicMin(&best_one, st0 + tid);
+        __syncthreads();
+        if (best_one <= chunk_keep_tiles(pf_tiles, a.hkv, 0)) split_tiles = best_one;
+      }
     } else {
-      split_tiles = refine_split_tiles(st0, tm.y, chunk_wgs);
+      split_tiles = refine_split_tiles(st0, tm.y, chunk_keep_tiles(pf_tiles, a.hkv, 0), chunk_wgs);
     }
   }
 
@@ -2045,7 +2075,8 @@ int hx_varlen_attn_count_items(const int32_t* q_lens, const int32_t* k_lens, int
     }
     return total * n_kv_heads;
   };
-  const int split_tiles = refine_split_tiles(chunk_split_tiles(tiles0, items0, n_kv_heads), max_tiles, chunk_wgs);
+  const int split_tiles = refine_split_tiles(chunk_split_tiles(tiles0, items0, n_kv_heads), max_tiles,
+                                             chunk_keep_tiles(tiles0, n_kv_heads, 0), chunk_wgs);
   const int keep_tiles = chunk_keep_tiles(tiles0, n_kv_heads, split_tiles);
   int64_t nd = 0, np = 0, nc = 0;
   for (int b = 0; b < batch; ++b) {

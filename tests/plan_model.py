@@ -15,7 +15,8 @@ has at most 256 row blocks, the chunk items are then reordered block by block, l
 first: by key tiles per item, descending, ties in that order. The split size
 follows the documented rule (at least max(8, ceil(tiles * Hkv / 512)) tiles when the
 unsplit chunk items launch fewer than 512 workgroups, raised to the smallest size that
-fits whole rounds of 256 workgroups); then only blocks longer than max(split size,
+fits whole rounds of 256 workgroups, or one round when the size that fits one round is
+at most 1.25 x the chunk tiles per CU); then only blocks longer than max(split size,
 1.25 x the chunk tiles per CU) split. The workspace offsets mirror make_layout.
 """
 
@@ -82,10 +83,16 @@ def split_tiles(q_lens, k_lens, hq: int, hkv: int, window) -> int:
     max_t = max(blocks)
     if max_t <= st:
         return st
+    st0 = st
     w0 = wgs(st)
     rounds = w0 // CUS
     if rounds >= 1 and w0 % CUS and wgs(max_t) <= rounds * CUS:
-        st = min(s for s in range(st, max_t + 1) if wgs(s) <= rounds * CUS)
+        st = min(s for s in range(st0, max_t + 1) if wgs(s) <= rounds * CUS)
+    # one round instead, when its pieces are no longer than 1.25 x the tiles per CU
+    if w0 > CUS and wgs(max_t) <= CUS:
+        s1 = min(s for s in range(st0, max_t + 1) if wgs(s) <= CUS)
+        if s1 <= _ceil(5 * sum(blocks) * quads * hkv, 4 * CUS):
+            st = s1
     return st
 
 

@@ -61,8 +61,9 @@ def _expected_counts(w: synth.Workload, window=(-1, 0)):
     each block's 64-key tiles are cut into splits of at least max(8, ceil(tiles * Hkv /
     512)) tiles, every split row adding one combine record. When the split workgroups
     spill past R >= 1 whole rounds of 256 (one chunk workgroup per CU), the split size is
-    the smallest one, up to the largest block's tiles, whose count fits R rounds. Then
-    only blocks longer than max(split size, ceil(1.25 x chunk tiles x Hkv / 256)) split."""
+    the smallest one, up to the largest block's tiles, whose count fits R rounds, or one
+    round when that size is at most ceil(1.25 x chunk tiles x Hkv / 256). Then only
+    blocks longer than max(split size, ceil(1.25 x chunk tiles x Hkv / 256)) split."""
     nd = nc = npf = 0
     G = w.n_q_heads // w.n_kv_heads
     gw = min(G, 4)
@@ -91,10 +92,15 @@ def _expected_counts(w: synth.Workload, window=(-1, 0)):
         return w.n_kv_heads * quads * sum(split_count(tiles(*blk), st) for blk in blocks)
 
     if split:
-        w0 = wgs(split)
+        st0, w0 = split, wgs(split)
         rounds, max_t = w0 // 256, max(tiles(*blk) for blk in blocks)
-        if rounds >= 1 and w0 % 256 and max_t > split and wgs(max_t) <= rounds * 256:
-            split = min(st for st in range(split, max_t + 1) if wgs(st) <= rounds * 256)
+        if rounds >= 1 and w0 % 256 and max_t > st0 and wgs(max_t) <= rounds * 256:
+            split = min(st for st in range(st0, max_t + 1) if wgs(st) <= rounds * 256)
+        # one round instead when its split size is at most 1.25 x the tiles per CU
+        if w0 > 256 and max_t > st0 and wgs(max_t) <= 256:
+            s1 = min(st for st in range(st0, max_t + 1) if wgs(st) <= 256)
+            if s1 <= -(-5 * tiles0 * w.n_kv_heads // (4 * 256)):
+                split = s1
     keep = max(split, -(-5 * tiles0 * w.n_kv_heads // (4 * 256)))
     for n, L in zip(w.q_lens, w.k_lens):
         if n == 1:
@@ -130,7 +136,7 @@ def test_chunk_splits_fill_whole_rounds(chunks):
     counts = ops.count_items(q_lens, k_lens, 32, 8, (-1, 0))
     assert counts == _expected_counts(w)
     # Without the refinement most of these spill to 536-696 workgroups (a partial third
-    # round); with it every one fits two rounds.
+    # round); with it every one fits two rounds (or one).
     assert counts[1] * 8 <= 512
 
 
