@@ -192,3 +192,16 @@ def test_noalloc_rejects_a_tick_beyond_its_scratch():
     args[21] = 100   # head_dim
     assert lib.hx_varlen_attn_noalloc(*args) == _capi.HX_E_UNSUPPORTED
     assert "no-allocation scratch" in _capi.strerror(_capi.HX_E_TOO_LARGE)
+
+
+def test_chunk_split_policy_known_answers():
+    """The planner's split choices on three tick shapes, as workgroup counts (items x 8 KV
+    heads): C3's blocks of up to 16 tiles stay whole and the 8 longer ones per KV head
+    split in three (384); a 1024-row chunk at position 4096 (blocks of 65-80 tiles)
+    splits once per block into one round (256); C4 does not split (512)."""
+    c3 = synth.c3()
+    assert ops.count_items(c3.q_lens, c3.k_lens, 32, 8, (-1, 0))[1] * 8 == 384
+    q_lens, k_lens = [1024] + [1] * 4, [5120, 700, 1300, 257, 4096]
+    assert ops.count_items(q_lens, k_lens, 32, 8, (-1, 0))[1] * 8 == 256
+    c4 = synth.c4()
+    assert ops.count_items(c4.q_lens, c4.k_lens, 32, 8, (-1, 0))[1] * 8 == 512
