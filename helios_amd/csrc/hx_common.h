@@ -113,6 +113,45 @@ __device__ __forceinline__ uint4 ld16_stream(const void* p) {
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// Raw buffer resource over `bytes` bytes from `base` (stride 0: byte addressing, reads
+// past `bytes` return zeros), for loads whose per-lane part is a 32-bit offset and whose
+// per-load part is a scalar offset: no per-load vector address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// 16-byte buffer load at byte offset voff + soff with the non-temporal hint (aux bit 1).
+__device__ __forceinline__ uint4 ld16_stream(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 2));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// a.lo*b.lo + a.hi*b.hi in fp32 with a zero accumulator, as the three-operand dot2 with an
+// inline 0: the two-operand form ties the accumulator to the destination and needs a
+// v_mov of 0 first.
+template <typename T>
+__device__ __forceinline__ float dot2_zero(uint32_t a, uint32_t b);
+template <>
+__device__ __forceinline__ float dot2_zero<__bf16>(uint32_t a, uint32_t b) {
+  float r;
+  asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+template <>
+__device__ __forceinline__ float dot2_zero<_Float16>(uint32_t a, uint32_t b) {
+  float r;
+  asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+// 8 packed elements . 8 packed elements, in fp32 (four dot2 steps from zero).
+template <typename T>
+__device__ __forceinline__ float dot8_zero(uint4 a, uint4 b) {
+  float c = dot2_zero<T>(a.x, b.x);
+  c = Elem<T>::dot2(a.y, b.y, c);
+  c = Elem<T>::dot2(a.z, b.z, c);
+  return Elem<T>::dot2(a.w, b.w, c);
+}
+
 // 8 packed elements . 8 packed elements + c, in fp32 (four dot2 steps).
 template <typename T>
 __device__ __forceinline__ float dot8(uint4 a, uint4 b, float c) {
@@ -120,6 +159,28 @@ __device__ __forceinline__ float dot8(uint4 a, uint4 b, float c) {
   c = Elem<T>::dot2(a.y, b.y, c);
   c = Elem<T>::dot2(a.z, b.z, c);
   return Elem<T>::dot2(a.w, b.w, c);
+}
+
+// Per-lane select by a wave-uniform 64-bit lane mask held in scalar registers: lanes whose
+// mask bit is set take a, the others b. Written as the three-operand v_cndmask_b32 so the
+// mask stays in an SGPR pair: the compiler otherwise picks the two-operand form that
+// reads VCC, which issues about 4x slower on gfx950.
+__device__ __forceinline__ float lane_sel(uint64_t mask, float a, float b) {
+  float r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(b), "v"(a), "s"(mask));
+  return r;
+}
+__device__ __forceinline__ uint32_t lane_sel(uint64_t mask, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(b), "v"(a), "s"(mask));
+  return r;
+}
+// Lanes whose index within their 16-lane row has `bit` set.
+__device__ __forceinline__ constexpr uint64_t row_bit_lanes(int bit) {
+  uint64_t m = 0;
+  for (int l = 0; l < 64; ++l)
+    if ((l & 15) >> bit & 1) m |= 1ull << l;
+  return m;
 }
 
 // Cross-lane moves within a 16-lane row (DPP). Each pairing is an involution:

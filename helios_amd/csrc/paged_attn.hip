@@ -11,10 +11,12 @@
 //                   work lists into the workspace. Run once per tick, reused per layer.
 //   decode_kernel   one workgroup per (256-key split, KV head). The G query heads of the
 //                   KV group share one read of the split's K and V (64 KiB each at
-//                   Qwen3-4B shape), streamed as whole 256-byte rows per 16-lane group.
+//                   Qwen3-4B shape), streamed by buffer loads as whole 256-byte rows per
+//                   16-lane group, the four waves interleaved over 16-token blocks.
 //                   QK^T runs on VALU dot2 with a DPP reduce-scatter across the 16 lanes;
-//                   softmax uses DPP wave reductions plus a 4-wave LDS step; PV runs on
-//                   VALU in fp32.
+//                   each wave keeps its own softmax max and sum; PV runs on VALU dot2
+//                   over token pairs with P rounded to the element type; the waves'
+//                   (max, sum, o) merge once through LDS.
 //                   A sequence that fits one split writes its output directly; longer ones
 //                   write partials: fp32 (m, l) and o / l rounded to the element type (the
 //                   partial stores cost more than their 1.6% of the bytes suggests, so they
@@ -922,10 +924,12 @@ __device__ __forceinline__ uint4 ld16(const T* p) {
 // Reduce-scatter across the 16 lanes of a row group: lane c holds partial dot products
 // part[i][h] of rows i = 0..15 over its own 8 dims; afterwards out[h] is the full dot
 // product of row c. Four DPP butterfly steps (mirror, half-mirror, xor 2, xor 1), each
-// pairing lanes that differ in one more bit of c and agree on the bits already used.
+// pairing lanes that differ in one more bit of c and agree on the bits already used; the
+// half a lane keeps is chosen by a bit select on that bit of c.
 template <int G>
 __device__ __forceinline__ void row_reduce_scatter(float (&part)[16][G], float (&out)[G], int c) {
-  const bool b3 = c & 8, b2 = c & 4, b1 = c & 2, b0 = c & 1;
+  constexpr uint64_t b3 = hx::row_bit_lanes(3), b2 = hx::row_bit_lanes(2), b1 = hx::row_bit_lanes(1),
+                     b0 = hx::row_bit_lanes(0);
   float s8[8][G], s4[4][G], s2[2][G];
 #pragma unroll
   for (int j = 0; j < 8; ++j)
@@ -933,7 +937,7 @@ __device__ __forceinline__ void row_reduce_scatter(float (&part)[16][G], float (
     for (int h = 0; h < G; ++h) {
       const float lo = part[j][h] + hx::dpp<hx::kDppMirror>(part[j][h]);
       const float hi = part[j + 8][h] + hx::dpp<hx::kDppMirror>(part[j + 8][h]);
-      s8[j][h] = b3 ? hi : lo;
+      s8[j][h] = hx::lane_sel(b3, hi, lo);
     }
 #pragma unroll
   for (int j = 0; j < 4; ++j)
@@ -941,7 +945,7 @@ __device__ __forceinline__ void row_reduce_scatter(float (&part)[16][G], float (
     for (int h = 0; h < G; ++h) {
       const float lo = s8[j][h] + hx::dpp<hx::kDppHalfMirror>(s8[j][h]);
       const float hi = s8[j + 4][h] + hx::dpp<hx::kDppHalfMirror>(s8[j + 4][h]);
-      s4[j][h] = b2 ? hi : lo;
+      s4[j][h] = hx::lane_sel(b2, hi, lo);
     }
 #pragma unroll
   for (int j = 0; j < 2; ++j)
@@ -949,13 +953,13 @@ __device__ __forceinline__ void row_reduce_scatter(float (&part)[16][G], float (
     for (int h = 0; h < G; ++h) {
       const float lo = s4[j][h] + hx::dpp<hx::kDppXor2>(s4[j][h]);
       const float hi = s4[j + 2][h] + hx::dpp<hx::kDppXor2>(s4[j + 2][h]);
-      s2[j][h] = b1 ? hi : lo;
+      s2[j][h] = hx::lane_sel(b1, hi, lo);
     }
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     const float lo = s2[0][h] + hx::dpp<hx::kDppXor1>(s2[0][h]);
     const float hi = s2[1][h] + hx::dpp<hx::kDppXor1>(s2[1][h]);
-    out[h] = b0 ? hi : lo;
+    out[h] = hx::lane_sel(b0, hi, lo);
   }
 }
 
@@ -999,27 +1003,46 @@ __device__ void append_rows(const RunArgs& a, int wg, int n_wg) {
   }
 }
 
+// Broadcast lane `SRC` of each 16-lane row to the whole row (DPP row_newbcast).
+template <int SRC>
+__device__ __forceinline__ uint32_t row_bcast(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x150 + SRC, 0xF, 0xF, false);
+}
+
+// Sum over the four 16-lane rows of a wave, scattered: x[v] (NV values per lane) becomes
+// NV / 4 values per lane, lane row q holding the sums of x[q * NV / 4 + k]. Two
+// permlane-swap steps; each swap exchanges half a register pair, so one swap and one add
+// produce one reduced value.
+template <int NV>
+__device__ __forceinline__ void rows_reduce_scatter(const float (&x)[NV], float (&z)[NV / 4]) {
+  float y[NV / 2];
+#pragma unroll
+  for (int k = 0; k < NV / 2; ++k) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[k]), __float_as_uint(x[k + NV / 2]), false, false);
+    y[k] = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+  }
+#pragma unroll
+  for (int k = 0; k < NV / 4; ++k) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(y[k]), __float_as_uint(y[k + NV / 4]), false, false);
+    z[k] = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+  }
+}
+
 // APPEND_ROWS: the launch also holds the append workgroups (a.app_wgs after the decode
 // workgroups); a separate instantiation, so decode-only launches carry no trace of them.
-// Occupancy: three workgroups per CU (168 VGPRs) up to G = 4. The bf16 builds fit that by
-// themselves; the fp16 builds need the bound (170 VGPRs and two workgroups without it,
-// 11 % slower at C2), and get it alone so that the bf16 code is unchanged.
+// Occupancy: three workgroups per CU (at most 168 VGPRs) up to G = 4.
 template <typename T, int G>
 constexpr int decode_min_wgs() {
-  return G <= 4 && std::is_same<T, _Float16>::value ? 3 : 2;
+  return G <= 4 ? 3 : 2;
 }
 template <typename T, int G, bool APPEND_ROWS>
 __global__ __launch_bounds__(kThreads, (decode_min_wgs<T, G>())) void decode_kernel(RunArgs a) {
   typedef hx::Elem<T> E;
-  constexpr int GP = G <= 4 ? 4 : 8;      // floats per token in p_lds
-  __shared__ __attribute__((aligned(16))) float p_lds[kSplit * GP];
-  __shared__ float red_max[4][8];
-  __shared__ float red_sum[4][8];
-  // Row stride kThreads + 8 floats: the 64 lanes of a wave reading (e, c) pairs of the
-  // final sum hit 64 distinct banks.
-  __shared__ float red_o[G * 8][kThreads + 8];
-  __shared__ float fin_m[8];
-  __shared__ float fin_l[8];
+  constexpr int NV = G * 8;  // o values per lane: G heads x 8 dims
+  // Per wave: max and sum of its 64 keys (log2 units), and its o summed over its rows.
+  __shared__ float w_max[4][G];
+  __shared__ float w_sum[4][G];
+  __shared__ __attribute__((aligned(16))) float w_o[4][G * kD];
 
   const int tid = hx::tid_x(), lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, held in a scalar register
@@ -1071,9 +1094,10 @@ __global__ __launch_bounds__(kThreads, (decode_min_wgs<T, G>())) void decode_ker
   const T* vbase = reinterpret_cast<const T*>(a.v) + row0 * a.kv_row + (int64_t)g * a.kv_head;
 
   // Lane (r, c) = (lane / 16, lane % 16) owns the 16-byte chunk c (dims 8c..8c+7) of
-  // tokens 64w + 4i + r, i = 0..15: every wave instruction reads four whole 256-byte
-  // head rows, the access pattern that streams at full HBM rate (16 rows x 64 B per
-  // instruction, the MFMA fragment layout, does not).
+  // tokens 16i + 4w + r, i = 0..15: every wave instruction reads four whole 256-byte head
+  // rows, and the four waves' i-th loads together read 16 consecutive tokens. Reading
+  // the split front to back this way streams about 5 % faster than giving each wave a
+  // contiguous quarter of the split.
   const int r = lane >> 4, c = lane & 15;
   uint4 qf[G];
   {
@@ -1081,172 +1105,188 @@ __global__ __launch_bounds__(kThreads, (decode_min_wgs<T, G>())) void decode_ker
 #pragma unroll
     for (int h = 0; h < G; ++h) qf[h] = ld16(qp + (int64_t)h * a.q_head);
   }
-  // Rows outside [kb, ke) re-read the split's first visible row (same cache lines,
-  // always inside the buffer): that data is finite, its score is masked to -inf below
-  // and its p is 0, so it needs no zeroing and all 32 loads issue back to back under one
-  // uniform branch. An empty split (no visible key, or a bad page id) loads nothing and
-  // uses zero registers.
-  uint4 kr[16], vr[16];
   const bool any = page_ok && kb < ke;
-  const int nfirst = kb - key0;
   const int nend = ke - key0;
-  if (any) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int n = 64 * w + 4 * i + r;
-      kr[i] = hx::ld16_stream(kbase + ((n >= nfirst && n < nend) ? n : nfirst) * kvr + 8 * c);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int n = 64 * w + 4 * i + r;
-      vr[i] = hx::ld16_stream(vbase + ((n >= nfirst && n < nend) ? n : nfirst) * kvr + 8 * c);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      kr[i] = hx::zero4();
-      vr[i] = hx::zero4();
-    }
-  }
 
   // Fused append (decode rows only): the split holding key L-1, this row's new token,
-  // takes that token's K/V from k_new / v_new instead of the pool and writes it to pool
-  // row write_slots[q0] (the 16 lanes owning the token each store their 16-byte chunk
-  // of head g). No other workgroup reads that pool row during this launch.
+  // writes that token's K/V from k_new / v_new to pool row write_slots[q0] (the 16 lanes
+  // that load the token's row each store their 16-byte chunk of head g), waits for the
+  // stores, and then reads the row from the pool like every other key, as the reference
+  // reads its pool after _write. No other workgroup reads that slice of the row during
+  // this launch.
   if (a.k_new != nullptr && L >= 1 && L - 1 >= key0 && L - 1 < key0 + kSplit) {
     const int nn = L - 1 - key0;
-    const bool owner = (nn >> 6) == w && (nn & 3) == r;
-    const int i_new = (nn & 63) >> 2;
-    const uint4 knew = ld16(reinterpret_cast<const T*>(a.k_new) + (int64_t)q0 * a.kn_row +
-                            (int64_t)g * a.kn_head + 8 * c);
-    const uint4 vnew = ld16(reinterpret_cast<const T*>(a.v_new) + (int64_t)q0 * a.vn_row +
-                            (int64_t)g * a.vn_head + 8 * c);
-    if (owner) {
-      const int64_t slot = a.write_slots[q0];
-      if (slot >= 0 && slot < a.pool_rows) {
-        const int64_t off = slot * a.kv_row + (int64_t)g * a.kv_head + 8 * c;
-        *reinterpret_cast<uint4*>(const_cast<uint8_t*>(a.k) + off * (int64_t)sizeof(T)) = knew;
-        *reinterpret_cast<uint4*>(const_cast<uint8_t*>(a.v) + off * (int64_t)sizeof(T)) = vnew;
+    if (((nn >> 2) & 3) == w) {  // wave-uniform: this wave loads the token's row
+      if ((nn & 3) == r) {
+        const int64_t slot = a.write_slots[q0];
+        if (slot >= 0 && slot < a.pool_rows) {
+          const T* kp = reinterpret_cast<const T*>(a.k_new) + (int64_t)q0 * a.kn_row + (int64_t)g * a.kn_head + 8 * c;
+          const T* vp = reinterpret_cast<const T*>(a.v_new) + (int64_t)q0 * a.vn_row + (int64_t)g * a.vn_head + 8 * c;
+          const int64_t off = slot * a.kv_row + (int64_t)g * a.kv_head + 8 * c;
+          *reinterpret_cast<uint4*>(const_cast<uint8_t*>(a.k) + off * (int64_t)sizeof(T)) = ld16(kp);
+          *reinterpret_cast<uint4*>(const_cast<uint8_t*>(a.v) + off * (int64_t)sizeof(T)) = ld16(vp);
+        }
       }
-    }
-    // When the new token is the split's only visible key (nfirst == nn), every masked
-    // row re-read that token's pool row, which this launch has not written yet: stale
-    // page contents, possibly not finite, that p = 0 would turn into NaN. All rows take
-    // the new token's values instead (masked rows need any finite data).
-    const bool alone = nfirst == nn;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (alone || (i == i_new && owner)) {
-        kr[i] = knew;
-        vr[i] = vnew;
-      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
   }
 
-  // q . k on VALU (packed dot2, fp32 accumulate), then the 16 lanes of each row group
-  // exchange partial sums so that lane (r, c) ends with token 64w + 4c + r.
-  float part[16][G];
+  // Per wave: max and sum of p over its keys (log2 units), and o = P V. An empty split
+  // (no visible key, or a bad page id) loads nothing and keeps (-inf, 0, 0).
+  float mx[G], ps[G], o[G][8];
+  if (any) {
+    // Buffer loads at a 32-bit lane offset plus a scalar step of 16 rows per load: no
+    // per-load vector address work. The resource ends after the split's last visible row,
+    // so rows past it read zeros (the range check covers the scalar offset too); rows
+    // before the first visible one (a window's start) are earlier keys of the sequence.
+    // Either way the data is finite, and its score is masked below. Offsets stay below
+    // 2^32: the host caps the row stride at 2^23 elements (the range is clamped to fit).
+    uint4 kr[16], vr[16];
+    const uint32_t row_bytes = (uint32_t)kvr * (uint32_t)sizeof(T);
+    const uint32_t loff = (uint32_t)(4 * w + r) * row_bytes + 16u * (uint32_t)c;
+    const uint32_t step = 16u * row_bytes;
+    const uint64_t span = (uint64_t)nend * row_bytes;
+    const uint32_t range = span > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)span;
+    const __amdgpu_buffer_rsrc_t kres = hx::buffer_rsrc(kbase, range);
+    const __amdgpu_buffer_rsrc_t vres = hx::buffer_rsrc(vbase, range);
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
+    for (int i = 0; i < 16; ++i) kr[i] = hx::ld16_stream(kres, loff, (uint32_t)i * step);
 #pragma unroll
-    for (int h = 0; h < G; ++h) part[i][h] = hx::dot8<T>(qf[h], kr[i], 0.f);
-  float sc[G];
-  row_reduce_scatter<G>(part, sc, c);
+    for (int i = 0; i < 16; ++i) vr[i] = hx::ld16_stream(vres, loff, (uint32_t)i * step);
 
-  const int t = 64 * w + 4 * c + r;
-  const bool tok_ok = page_ok && key0 + t >= kb && key0 + t < ke;
-  float mx[G];
+    // q . k on VALU (packed dot2, fp32 accumulate), then the 16 lanes of each row group
+    // exchange partial sums so that lane (r, c) ends with token 16c + 4w + r.
+    float part[16][G];
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    sc[h] = tok_ok ? sc[h] * a.scale_log2 : -INFINITY;
-    mx[h] = wave_max(sc[h]);
-  }
-  if (lane == 0) {
+    for (int i = 0; i < 16; ++i)
 #pragma unroll
-    for (int h = 0; h < G; ++h) red_max[w][h] = mx[h];
-  }
-  __syncthreads();
-  float ps[G];
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const float m = fmaxf(fmaxf(red_max[0][h], red_max[1][h]), fmaxf(red_max[2][h], red_max[3][h]));
-    const float p = sc[h] == -INFINITY ? 0.f : hx::fast_exp2(sc[h] - m);
-    sc[h] = p;
-    ps[h] = wave_sum(p);
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) red_sum[w][h] = ps[h];
-  }
-  if (G >= 4) {
-#pragma unroll
-    for (int h = 0; h < G; h += 4)
-      *reinterpret_cast<float4*>(&p_lds[t * GP + h]) = make_float4(sc[h], sc[h + 1], sc[h + 2], sc[h + 3]);
-  } else {
-#pragma unroll
-    for (int h = 0; h < G; ++h) p_lds[t * GP + h] = sc[h];
-  }
-  __syncthreads();
+      for (int h = 0; h < G; ++h) part[i][h] = hx::dot8_zero<T>(qf[h], kr[i]);
+    float sc[G];
+    row_reduce_scatter<G>(part, sc, c);
 
-  // O = P V on VALU, fp32 accumulate: row 64w+4i+r of V meets p of the same token.
-  float o[G][8];
+    // Softmax inside the wave: its own max (no barrier), p = 2^(s - max) rounded to the
+    // element type, and the sum of the rounded p, so that o / l is exactly the average of
+    // V under the weights that multiply it. The waves' (max, sum, o) merge at the end.
+    const int t = 16 * c + 4 * w + r;
+    const bool tok_ok = key0 + t >= kb && key0 + t < ke;
+    uint32_t pp[G];  // {p of token 16c' + 4w + r, p of token 16(c'+1) + 4w + r}, c' = c & ~1
+    constexpr uint64_t odd = hx::row_bit_lanes(0);
 #pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int n = 64 * w + 4 * i + r;
-    float pv[GP];
-#pragma unroll
-    for (int j = 0; j < GP; j += 4) {
-      const float4 t4 = *reinterpret_cast<const float4*>(&p_lds[n * GP + j]);
-      pv[j] = t4.x;
-      pv[j + 1] = t4.y;
-      pv[j + 2] = t4.z;
-      pv[j + 3] = t4.w;
+    for (int h = 0; h < G; ++h) {
+      const float x = tok_ok ? sc[h] * a.scale_log2 : -INFINITY;
+      mx[h] = wave_max(x);
+      const float p = x == -INFINITY ? 0.f : hx::fast_exp2(x - mx[h]);
+      const float q = hx::dpp<hx::kDppXor1>(p);
+      pp[h] = hx::pack2_round<T>(hx::lane_sel(odd, q, p), hx::lane_sel(odd, p, q));
+      ps[h] = wave_sum(E::lo(hx::lane_sel(odd, pp[h] >> 16, pp[h])));
     }
-    const uint4 vv = vr[i];
-    const float vf[8] = {E::lo(vv.x), E::hi(vv.x), E::lo(vv.y), E::hi(vv.y),
-                         E::lo(vv.z), E::hi(vv.z), E::lo(vv.w), E::hi(vv.w)};
+
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[h][e] = fmaf(pv[h], vf[e], o[h][e]);
+      for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+    // O = P V with dot2 over token pairs: pair j is tokens 32j + 4w + r and
+    // 32j + 16 + 4w + r (loads 2j and 2j + 1 of this lane); its p pair sits in lane 2j
+    // of the row.
+#define HX_PV_PAIR(J)                                                                          \
+  {                                                                                            \
+    uint32_t pb[G];                                                                            \
+    _Pragma("unroll") for (int h = 0; h < G; ++h) pb[h] = row_bcast<2 * (J)>(pp[h]);           \
+    const uint4 v0 = vr[2 * (J)], v1 = vr[2 * (J) + 1];                                        \
+    const uint32_t vp[8] = {hx::interleave_lo(v0.x, v1.x), hx::interleave_hi(v0.x, v1.x),      \
+                            hx::interleave_lo(v0.y, v1.y), hx::interleave_hi(v0.y, v1.y),      \
+                            hx::interleave_lo(v0.z, v1.z), hx::interleave_hi(v0.z, v1.z),      \
+                            hx::interleave_lo(v0.w, v1.w), hx::interleave_hi(v0.w, v1.w)};     \
+    _Pragma("unroll") for (int h = 0; h < G; ++h)                                              \
+      _Pragma("unroll") for (int e = 0; e < 8; ++e) o[h][e] = E::dot2(pb[h], vp[e], o[h][e]); \
   }
+    HX_PV_PAIR(0) HX_PV_PAIR(1) HX_PV_PAIR(2) HX_PV_PAIR(3)
+    HX_PV_PAIR(4) HX_PV_PAIR(5) HX_PV_PAIR(6) HX_PV_PAIR(7)
+#undef HX_PV_PAIR
+  } else {
 #pragma unroll
-  for (int h = 0; h < G; ++h)
+    for (int h = 0; h < G; ++h) {
+      mx[h] = -INFINITY;
+      ps[h] = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) red_o[h * 8 + e][tid] = o[h][e];
-  if (tid < G) {
-    float mm = -INFINITY, ll = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
-      mm = fmaxf(mm, red_max[ww][tid]);
-      ll += red_sum[ww][tid];
+      for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
     }
-    fin_m[tid] = mm;
-    fin_l[tid] = ll;
+  }
+
+  // The wave's o summed over its four rows: lane row r keeps values v = r*2G .. r*2G+2G-1
+  // of v = 8h + e, i.e. head v / 8, dims 8c + v % 8.
+  {
+    float x[NV];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[h * 8 + e] = o[h][e];
+    float z[NV / 4];
+    rows_reduce_scatter<NV>(x, z);
+    constexpr int NQ = NV / 4;
+    if constexpr (NQ % 4 == 0) {
+#pragma unroll
+      for (int k = 0; k < NQ; k += 4) {
+        const int v = r * NQ + k;
+        *reinterpret_cast<float4*>(&w_o[w][(v >> 3) * kD + 8 * c + (v & 7)]) = make_float4(z[k], z[k + 1], z[k + 2], z[k + 3]);
+      }
+    } else {
+      const int v = r * NQ;
+      *reinterpret_cast<float2*>(&w_o[w][(v >> 3) * kD + 8 * c + (v & 7)]) = make_float2(z[0], z[1]);
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      w_max[w][h] = mx[h];
+      w_sum[w][h] = ps[h];
+    }
   }
   __syncthreads();
 
-  for (int oi = tid; oi < G * kD; oi += kThreads) {
-    const int h = oi >> 7, d = oi & (kD - 1), cc = d >> 3, e = d & 7;
-    float acc = 0.f;
+  // G x 16 lanes finish: lane f = 16h + cc merges head h, dims 8cc..8cc+7 over the four
+  // waves and stores them as one 16-byte row piece.
+  if (tid < G * 16) {
+    const int h = tid >> 4, cc = tid & 15;
+    float m = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww)
+    for (int ww = 0; ww < 4; ++ww) m = fmaxf(m, w_max[ww][h]);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float l = 0.f;
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) acc += red_o[h * 8 + e][ww * 64 + rr * 16 + cc];
-    const float mh = fin_m[h], lh = fin_l[h];
+    for (int ww = 0; ww < 4; ++ww) {
+      const float mw = w_max[ww][h];
+      const float alpha = mw == -INFINITY ? 0.f : hx::fast_exp2(mw - m);
+      l = fmaf(alpha, w_sum[ww][h], l);
+      const float4 a0 = *reinterpret_cast<const float4*>(&w_o[ww][h * kD + 8 * cc]);
+      const float4 a1 = *reinterpret_cast<const float4*>(&w_o[ww][h * kD + 8 * cc + 4]);
+      acc[0] = fmaf(alpha, a0.x, acc[0]);
+      acc[1] = fmaf(alpha, a0.y, acc[1]);
+      acc[2] = fmaf(alpha, a0.z, acc[2]);
+      acc[3] = fmaf(alpha, a0.w, acc[3]);
+      acc[4] = fmaf(alpha, a1.x, acc[4]);
+      acc[5] = fmaf(alpha, a1.y, acc[5]);
+      acc[6] = fmaf(alpha, a1.z, acc[6]);
+      acc[7] = fmaf(alpha, a1.w, acc[7]);
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const uint4 val = make_uint4(hx::pack2_round<T>(acc[0] * inv, acc[1] * inv), hx::pack2_round<T>(acc[2] * inv, acc[3] * inv),
+                                 hx::pack2_round<T>(acc[4] * inv, acc[5] * inv), hx::pack2_round<T>(acc[6] * inv, acc[7] * inv));
     const int qh = g * G + h;
     if (splits == 1) {
-      const float val = lh > 0.f ? acc / lh : 0.f;
-      reinterpret_cast<uint16_t*>(a.out)[(int64_t)q0 * a.o_row + (int64_t)qh * a.o_head + d] = E::bits(val);
-      if (a.lse && d == 0)
-        a.lse[(int64_t)qh * a.total_q + q0] = lh > 0.f ? (mh + log2f(lh)) * kLn2 : -INFINITY;
+      T* orow = reinterpret_cast<T*>(a.out) + (int64_t)q0 * a.o_row + (int64_t)qh * a.o_head + 8 * cc;
+      if (a.o_row % 8 == 0 && a.o_head % 8 == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0) {
+        *reinterpret_cast<uint4*>(orow) = val;
+      } else {  // rows 8-byte aligned (checked on the host)
+        uint2* o2 = reinterpret_cast<uint2*>(orow);
+        o2[0] = make_uint2(val.x, val.y);
+        o2[1] = make_uint2(val.z, val.w);
+      }
+      if (a.lse && cc == 0)
+        a.lse[(int64_t)qh * a.total_q + q0] = l > 0.f ? (m + log2f(l)) * kLn2 : -INFINITY;
     } else {
-      a.part_o[((int64_t)item * a.hq + qh) * kD + d] = E::bits(lh > 0.f ? acc / lh : 0.f);
-      if (d == 0) a.part_ml[(int64_t)item * a.hq + qh] = make_float2(mh, lh);
+      *reinterpret_cast<uint4*>(a.part_o + ((int64_t)item * a.hq + qh) * kD + 8 * cc) = val;
+      if (cc == 0) a.part_ml[(int64_t)item * a.hq + qh] = make_float2(m, l);
     }
   }
 }
