@@ -5,8 +5,9 @@ new token's K/V of 64 sequences into a 2048-page x 256-token pool (bf16, 8 KV he
 head_dim 128), then paged GQA decode attention of 32 query heads over context lengths
 uniform in [512, 4096] (seeded), page tables drawn from a shuffled free list.
 Synthetic N(0, 1) data. Steps rotate over four layer pools (2 GiB each) so no step
-finds the previous step's pages in cache. The default 300 warm-up steps run past the
-speed ramp of a fresh process (its first ~200 steps are up to 12 % slower).
+finds the previous step's pages in cache. The defaults (20 timed steps after 5 warm-up
+steps) time the first ~3 ms of sustained decode work in a fresh process, when the shader
+clock is still settling (it dips about 9 % between ~1.5 and ~6 ms into the load).
 
 Printed JSON (one line):
   value     algorithmic HBM bytes per step / step time, in GB/s: every visible key's K
@@ -56,10 +57,8 @@ POOL_COPIES = 4
 def parse_args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
-    # A fresh process runs its first ~150-200 decode steps (~25 ms) at 114-127 us and then
-    # holds ~113 us: the default warm-up covers that, so the timed steps are steady state.
-    p.add_argument("--warmup", type=int, default=300)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-packed-tick", action="store_true")
     p.add_argument("--full-tick", action=argparse.BooleanOptionalAction, default=True,
