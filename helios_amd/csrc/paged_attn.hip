@@ -2307,12 +2307,15 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
     // Chunk rows (and every row of generic_kernel) read their own new keys from the
     // pool. When the tick may hold chunk rows and a decode launch runs on the tuned path,
     // workgroups added to that launch write every row (the chunk kernel runs after it,
-    // also in a later call); otherwise every row is appended first when chunk rows run.
+    // also in a later call); a decode-only tick's rows are written by their own decode
+    // workgroups; otherwise (chunk rows run, the generic kernel runs, or this call
+    // launches neither decode nor chunk work) every row is appended first, so that a
+    // call given new rows always writes them.
     const bool append_in_decode = tuned && max_q >= 2 && a.grid_dec > 0;
     if (append_in_decode) {
       const int64_t wgs = ((int64_t)total_q * n_kv_heads * (head_dim / 8) + kThreads - 1) / kThreads;
       a.app_wgs = (int32_t)(wgs < kAppendWGs ? wgs : kAppendWGs);
-    } else if (a.grid_pf > 0 || !tuned) {
+    } else if (a.grid_pf > 0 || !tuned || a.grid_dec == 0) {
       const int elem = 2;
       const int st2 = hx_kv_append(const_cast<void*>(k_cache), const_cast<void*>(v_cache), app->pool_rows,
                                    app->k_new, app->kn_row, app->kn_head, app->v_new, app->vn_row,

@@ -87,7 +87,7 @@ class PagedQwen3Decoder:
         reference's logits are computed and ``argmax`` taken."""
         config = self.config
         if input_ids.shape != (1, sum(cache.counts)):
-            raise ValueError("Packed input does not match query lengths.")
+            raise ValueError(f"input_ids must be [1, {sum(cache.counts)}]: one token per packed row of the tick.")
         hq, hkv, d = config.n_heads * config.head_dim, config.n_kv_heads * config.head_dim, config.head_dim
         eps = config.rms_norm_eps
         x = self.embedding[input_ids]

@@ -532,6 +532,11 @@ class VarlenAttnPlan:
         self.page_size = page_size
         self.block_table_stride = block_table_stride
         self.window = window
+        # The tuned kernels (split-K decode, MFMA chunk, combine) serve head_dim 128 with
+        # 1, 2, 4 or 8 query heads per KV head; other shapes run one generic kernel that
+        # covers every row in a single launch.
+        self.tuned = head_dim == 128 and n_kv_heads > 0 and n_q_heads % n_kv_heads == 0 \
+            and n_q_heads // n_kv_heads in (1, 2, 4, 8)
         self._metadata = (cu_seq_q.contiguous(), None if cu_seq_k is None else cu_seq_k.contiguous(),
                           None if seqused_k is None else seqused_k.contiguous())
         self.ws_bytes = workspace_bytes(max(batch, 0), max_q, max_k, n_q_heads, n_kv_heads, head_dim)
@@ -644,6 +649,12 @@ class VarlenAttnPlan:
             self.hints[1] if "chunk" in phases else 0,
             self.hints[2] if "combine" in phases else 0,
         )
+        if not self.tuned:
+            # The generic kernel covers every row in one launch: it runs in the call that
+            # holds the decode phase, or in the chunk phase of a tick without decode rows,
+            # never twice for one layer.
+            once = "decode" in phases or ("chunk" in phases and self.hints[0] == 0)
+            hints = (self.hints[0], self.hints[1], hints[2]) if once else (0, 0, hints[2])
         common = (
             query.data_ptr(), query.stride(0), query.stride(1),
             k_cache.data_ptr(), v_cache.data_ptr(), row_stride, head_stride,
@@ -688,10 +699,11 @@ def run_overlapped(plan: "VarlenAttnPlan", query: torch.Tensor, k_cache: torch.T
     must already be in the pool. ``side_first`` is an optional callable queued on the
     side stream before the chunk launch (work that must also overlap the decode rows);
     its return value is returned last, and any tensors in it are marked as used by the
-    current stream. Falls back to ``plan.run`` when one kind of row is absent."""
+    current stream. Falls back to ``plan.run`` when one kind of row is absent, and for
+    shapes the generic kernel serves (it covers every row in one launch)."""
     dec, pf, _ = plan.hints
     has_chunk = pf != 0 and plan.max_q >= 2
-    if dec == 0 or (not has_chunk and side_first is None):
+    if dec == 0 or (not has_chunk and side_first is None) or not plan.tuned:
         extra = side_first() if side_first is not None else None
         res = plan.run(query, k_cache, v_cache, block_table, return_lse=return_lse)
         return (res, extra) if side_first is not None else res
@@ -757,7 +769,7 @@ def varlen_attn(
     if n_q_heads != n_kv_heads and not enable_gqa:
         raise ValueError("Query and KV head counts differ; pass enable_gqa=True.")
     if n_kv_heads < 1 or n_q_heads % n_kv_heads:
-        raise ValueError("Query heads must be a multiple of KV heads for GQA.")
+        raise ValueError(f"GQA needs n_q_heads ({n_q_heads}) to be a multiple of n_kv_heads ({n_kv_heads}).")
     window = _window(window_size, is_causal)
     paged = block_table is not None
     if paged:

@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import gc
 
+import numpy as np
 import pytest
 import torch
 
@@ -51,6 +52,31 @@ def test_pool_validation_and_sizes():
     assert p.bytes_per_token == 2 * 2 * 1 * 8 * 4 and p.bytes_per_page == p.bytes_per_token * 256
     q = KVPagePool(Qwen3Config(n_layers=1), 1, device="meta")
     assert q.bytes_per_token == 4096  # 8 kv heads x 128 x bf16 x (K, V) for one layer
+
+
+def test_release_inside_acquire_loses_no_page(pool):
+    """A page released while ``acquire`` runs (the garbage collector can run a handle's
+    finaliser at any allocation, also between acquire's read of the free stack and its
+    update) is neither lost nor handed out twice, and comes back first afterwards."""
+    held = pool.acquire(3)
+    victim = [held.pop()]            # page 2: the only reference left is in this list
+    fired = []
+
+    class Trap(np.ndarray):
+        def __getitem__(self, key):  # acquire's read of the free stack
+            if victim:
+                victim.pop()         # drops the last reference: the release runs now
+                fired.append(True)
+            return np.ndarray.__getitem__(self, key)
+
+    pool._stack = pool._stack.view(Trap)
+    got = pool.acquire(2)
+    pool._stack = np.asarray(pool._stack)
+    assert fired, "the release ran inside acquire"
+    ids = [p.index for p in held + got]
+    assert ids == [0, 1, 3, 4] and len(set(ids)) == len(ids)
+    assert pool.free_pages + len(ids) == 6
+    assert [p.index for p in pool.acquire(1)] == [2]   # the id released last comes back first
 
 
 def test_free_list_is_lifo_from_page_zero(pool):

@@ -60,3 +60,26 @@ def test_noalloc_matches_workspace_entry_on_two_calls(device):
         ref, ref_lse = tick.oracle()
         compare(out_a, ref, what=f"noalloc {w.name}")
         assert np.abs(lse_a.cpu().numpy() - ref_lse).max() < 5e-3
+
+
+def test_noalloc_rejects_a_tick_beyond_the_scratch(device):
+    """A tick whose plan and partials exceed the 128 MiB scratch array (64 decode rows of
+    up to 2^20 keys: about 2.2 GB of split partials) is refused with HX_E_TOO_LARGE
+    before anything is launched: the output keeps its bits."""
+    lib = _capi.lib()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    w = synth.small_mixed(93, batch=3, max_cached=600, max_chunk=90, num_pages=32)
+    tick = DeviceTick(w, torch.bfloat16, device)
+    batch, max_q, max_k = 64, 1, 1 << 20
+    need = lib.hx_varlen_attn_workspace_bytes(batch, max_q, max_k, w.n_q_heads, w.n_kv_heads, w.head_dim)
+    assert need > 128 << 20
+    out = torch.full((w.total_q, w.n_q_heads, w.head_dim), float("nan"), dtype=torch.bfloat16, device=device)
+    lse = torch.full((w.n_q_heads, w.total_q), float("nan"), dtype=torch.float32, device=device)
+    before = out.clone()
+    args = _args(tick, out, lse)
+    args[14:18] = [batch, w.total_q, max_q, max_k]   # batch, total_q, max_q, max_k
+    torch.cuda.synchronize()
+    code = lib.hx_varlen_attn_noalloc(*args, stream)
+    assert code == _capi.HX_E_TOO_LARGE, _capi.strerror(code)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), before.view(torch.int16))
