@@ -152,6 +152,12 @@ __device__ __forceinline__ float dot8_zero(uint4 a, uint4 b) {
   return Elem<T>::dot2(a.w, b.w, c);
 }
 
+// 16-byte buffer load at byte offset voff (default cache policy).
+__device__ __forceinline__ uint4 ld16_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 // 8 packed elements . 8 packed elements + c, in fp32 (four dot2 steps).
 template <typename T>
 __device__ __forceinline__ float dot8(uint4 a, uint4 b, float c) {

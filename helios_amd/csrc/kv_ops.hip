@@ -76,6 +76,14 @@ struct CopyArgs {
   int32_t n_pages;
   int32_t tiles_per_page;
   int32_t n_wg;  // workgroups of the launch (the grid stride in tiles)
+  // Strided form (strided != 0): tensor t is layer t / per_layer's K (t % per_layer == 0)
+  // or V pool, at k0 / v0 + layer * layer_bytes; `tensors` is unused and n_tensors has
+  // no limit.
+  uint8_t* k0;
+  uint8_t* v0;
+  int64_t layer_bytes;
+  int32_t per_layer;
+  int32_t strided;
 };
 
 // Grid-stride over 16 KiB tiles of (tensor, page pair): each thread streams four
@@ -89,7 +97,8 @@ __global__ __launch_bounds__(kCopyThreads) void kv_copy_pages_kernel(CopyArgs a)
     const int64_t rest = t / a.tiles_per_page;
     const int pair = (int)(rest % a.n_pages);
     const int tensor = (int)(rest / a.n_pages);
-    uint8_t* base = a.tensors[tensor];
+    uint8_t* base = a.strided ? (tensor % a.per_layer == 0 ? a.k0 : a.v0) + (int64_t)(tensor / a.per_layer) * a.layer_bytes
+                              : a.tensors[tensor];
     const uint8_t* src = base + (int64_t)a.src[pair] * a.page_bytes;
     uint8_t* dst = base + (int64_t)a.dst[pair] * a.page_bytes;
     const int64_t t0 = (int64_t)tile * kCopyTileBytes;
@@ -271,15 +280,35 @@ int hx_kv_copy_pages(void* const* k_pools, void* const* v_pools, int32_t n_layer
   const int tiles = (int)((page_bytes + kCopyTileBytes - 1) / kCopyTileBytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int total_tensors = n_layers * per_layer;
-  for (int t0 = 0; t0 < total_tensors; t0 += kCopyMaxTensors) {
-    const int nt = total_tensors - t0 < kCopyMaxTensors ? total_tensors - t0 : kCopyMaxTensors;
+  // Pools of one allocation (every layer's K, and V, at one stride from the first, as a
+  // [2, layers, pages, ...] store lays them out) go in one launch whatever the layer
+  // count; other pointer lists go kCopyMaxTensors tensors per launch.
+  int64_t layer_bytes = 0;
+  bool strided = n_layers >= 2;
+  if (strided) {
+    layer_bytes = static_cast<uint8_t*>(k_pools[1]) - static_cast<uint8_t*>(k_pools[0]);
+    for (int l = 1; l < n_layers && strided; ++l) {
+      strided = static_cast<uint8_t*>(k_pools[l]) - static_cast<uint8_t*>(k_pools[0]) == (int64_t)l * layer_bytes &&
+                (!v_pools || static_cast<uint8_t*>(v_pools[l]) - static_cast<uint8_t*>(v_pools[0]) == (int64_t)l * layer_bytes);
+    }
+  }
+  const int per_launch = strided ? total_tensors : kCopyMaxTensors;
+  for (int t0 = 0; t0 < total_tensors; t0 += per_launch) {
+    const int nt = total_tensors - t0 < per_launch ? total_tensors - t0 : per_launch;
     for (int p0 = 0; p0 < n_pages; p0 += kCopyMaxPages) {
       const int np = n_pages - p0 < kCopyMaxPages ? n_pages - p0 : kCopyMaxPages;
       CopyArgs a;
-      for (int t = 0; t < nt; ++t) {
-        const int flat = t0 + t;
-        const int layer = flat / per_layer;
-        a.tensors[t] = static_cast<uint8_t*>((flat % per_layer == 0) ? k_pools[layer] : v_pools[layer]);
+      a.strided = strided ? 1 : 0;
+      a.per_layer = per_layer;
+      a.k0 = static_cast<uint8_t*>(k_pools[0]);
+      a.v0 = v_pools ? static_cast<uint8_t*>(v_pools[0]) : nullptr;
+      a.layer_bytes = layer_bytes;
+      if (!strided) {
+        for (int t = 0; t < nt; ++t) {
+          const int flat = t0 + t;
+          const int layer = flat / per_layer;
+          a.tensors[t] = static_cast<uint8_t*>((flat % per_layer == 0) ? k_pools[layer] : v_pools[layer]);
+        }
       }
       for (int p = 0; p < np; ++p) {
         a.src[p] = src_pages[p0 + p];

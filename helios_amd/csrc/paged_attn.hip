@@ -1582,15 +1582,17 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   // the next tile to load (pages hold a whole number of tiles).
   int ld_pi = pg_base, ld_off = paged ? t_begin * kTile - pg_base * a.page_size : 0;
 
-  // Per-thread element offsets of the rows this thread loads, relative to the tile's first
-  // row of KV head g.
-  const int kvr = (int)a.kv_row;
-  const int koff0 = kr_base * kvr + 8 * c16, koff1 = koff0 + 32 * kvr;
-  const int voff0 = 2 * vkp * kvr + 8 * c16, voff1 = voff0 + kvr;
+  // Per-thread byte offsets of the rows this thread loads, relative to the tile's first
+  // row of KV head g (the same for every tile).
+  const uint32_t row_bytes = (uint32_t)a.kv_row * (uint32_t)sizeof(T);
+  const uint32_t koff0 = (uint32_t)kr_base * row_bytes + 16u * (uint32_t)c16, koff1 = koff0 + 32u * row_bytes;
+  const uint32_t voff0 = (uint32_t)(2 * vkp) * row_bytes + 16u * (uint32_t)c16, voff1 = voff0 + row_bytes;
 
-  // Key rows past L - 1 (only in the last tile) load row L - 1 instead, which lies in the
-  // same page; their scores are masked to -inf, so no branch guards the loads. A bad page
-  // id reads page 0 and is reported in the error word.
+  // Each tile's K and V rows are read through buffer resources that end after the tile's
+  // last key (row L - 1 in the last tile): rows past it read zeros, whose scores are
+  // masked to -inf (the last tile is never "full"), so no branch or clamp guards the
+  // loads and a tile's addressing is scalar work. A bad page id reads page 0 and is
+  // reported in the error word.
   uint4 kreg[2], vreg[2];
   bool bad_page = false;  // some tile's page id was outside the pool
   auto load_tile = [&](int t) {
@@ -1619,18 +1621,13 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
     const int64_t head0 = rowb * a.kv_row + (int64_t)g * a.kv_head;
     const T* kt = reinterpret_cast<const T*>(a.k) + head0;
     const T* vt = reinterpret_cast<const T*>(a.v) + head0;
-    const int kmax = L - 1 - key_base;  // >= 0: key_base <= khi <= L - 1
-    if (kmax >= kTile - 1) {
-      kreg[0] = ld16(kt + koff0);
-      kreg[1] = ld16(kt + koff1);
-      vreg[0] = ld16(vt + voff0);
-      vreg[1] = ld16(vt + voff1);
-    } else {
-      kreg[0] = ld16(kt + min(kr_base, kmax) * kvr + 8 * c16);
-      kreg[1] = ld16(kt + min(kr_base + 32, kmax) * kvr + 8 * c16);
-      vreg[0] = ld16(vt + min(2 * vkp, kmax) * kvr + 8 * c16);
-      vreg[1] = ld16(vt + min(2 * vkp + 1, kmax) * kvr + 8 * c16);
-    }
+    const int rows = min(L - key_base, kTile);  // >= 1: key_base <= khi <= L - 1
+    const __amdgpu_buffer_rsrc_t kres = hx::buffer_rsrc(kt, (uint32_t)rows * row_bytes);
+    const __amdgpu_buffer_rsrc_t vres = hx::buffer_rsrc(vt, (uint32_t)rows * row_bytes);
+    kreg[0] = hx::ld16_buf(kres, koff0);
+    kreg[1] = hx::ld16_buf(kres, koff1);
+    vreg[0] = hx::ld16_buf(vres, voff0);
+    vreg[1] = hx::ld16_buf(vres, voff1);
   };
 
   if (t_begin < t_end) load_tile(t_begin);
@@ -1701,8 +1698,13 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (16 * kb + i < rlo || 16 * kb + i > rhi) sacc[kb][rb][i] = -INFINITY;
+          for (int i = 0; i < 4; ++i) {
+            // The lanes to mask as a lane mask in scalar registers, so the select is the
+            // fast three-operand form (hx::lane_sel).
+            const uint64_t hidden = __builtin_amdgcn_ballot_w64(16 * kb + i < rlo) |
+                                    __builtin_amdgcn_ballot_w64(16 * kb + i > rhi);
+            sacc[kb][rb][i] = hx::lane_sel(hidden, -INFINITY, sacc[kb][rb][i]);
+          }
       }
       // Row max on raw scores (the scale is positive), folded into exp2 by one FMA.
       float m = fmaxf(fmaxf(sacc[0][rb][0], sacc[0][rb][1]), fmaxf(sacc[0][rb][2], sacc[0][rb][3]));
