@@ -152,6 +152,24 @@ __device__ __forceinline__ float dot8_zero(uint4 a, uint4 b) {
   return Elem<T>::dot2(a.w, b.w, c);
 }
 
+// s_waitcnt immediate for vmcnt(0), other counters unconstrained (gfx9 encoding).
+constexpr unsigned kWaitVm0 = 0x0f70;
+
+// 16-byte buffer load at byte offset voff straight into LDS: lane l's bytes land at
+// lds_base + 16 l (lds_base wave-uniform). Completion is counted by vmcnt.
+__device__ __forceinline__ void ld16_to_lds(__amdgpu_buffer_rsrc_t r, void* lds_base, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base, 16, (int)voff, 0, 0, 0);
+}
+
+// ds_read_b64_tr_b16 at LDS byte address p. Within each 16-lane group the lanes' 8-byte
+// reads form a 4 x 16 block of 16-bit values (lane i supplies elements 4i..4i+3, row-major);
+// lane j of the group receives column j, i.e. elements j, 16 + j, 32 + j, 48 + j.
+__device__ __forceinline__ uint2 ld8_lds_tr16(const void* p) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+
 // 16-byte buffer load at byte offset voff (default cache policy).
 __device__ __forceinline__ uint4 ld16_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
   const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0));

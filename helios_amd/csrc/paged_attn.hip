@@ -23,8 +23,9 @@
 //                   are 16-bit; the extra error is one more rounding of the output in its
 //                   own precision).
 //   chunk_kernel    prefill chunks: 8 waves per workgroup (2 per SIMD), each wave owning
-//                   32 query rows of one head; 64-key K / V^T tiles go through LDS with a
-//                   register prefetch of the next tile; S^T = K Q^T and O^T = V^T P^T both
+//                   32 query rows of one head; 64-key K / V tiles are copied from HBM
+//                   straight into LDS (the next tile's copies in flight while the current
+//                   one is consumed; V read back transposed); S^T = K Q^T and O^T = V^T P^T both
 //                   run on 16x16x32 MFMA with online softmax in between. When the chunk
 //                   rows alone would not fill the GPU, row blocks are split over their key
 //                   tiles and write partials like decode splits.
@@ -1457,49 +1458,43 @@ __global__ __launch_bounds__(THREADS, 4) void combine_kernel(RunArgs a) {
 }
 
 // ------------------------------------------------------------------ chunk (prefill) MFMA
-constexpr int kKStride = kD + 8;       // K tile row: 136 elements (272 B)
-constexpr int kVStride = kTile + 8;    // V^T tile row: 72 elements (144 B = 36 dwords)
 constexpr int kChunkThreads = 512;     // 8 waves: 2 per SIMD
 constexpr float kLazyLog2 = 8.f;       // softmax terms stay <= 2^8 between max updates
-// Tile buffers: two K and two V^T tiles. Output staging after the tile loop: each
-// wave's 32 rows of one head (256 B each) at a 288-byte stride (72 dwords: the 16 rows x
-// 4 chunks one staging write covers fall on distinct bank pairs), in the same LDS.
-constexpr int kStageStride = 2 * kD + 32;
-constexpr int kTileLdsBytes = 2 * 2 * (kTile * kKStride + kD * kVStride);
-constexpr int kStageLdsBytes = 8 * 32 * kStageStride;
-constexpr int kChunkLdsBytes = kTileLdsBytes > kStageLdsBytes ? kTileLdsBytes : kStageLdsBytes;
-
-// V^T tile layout. Row d holds the 64 keys of dim d as 32 dwords (key pairs) in eight
-// 16-byte groups. Group 4*ks + q holds, in this order, keys 32ks + 4q + 0..3 and
-// 32ks + 16 + 4q + 0..3: the eight k-values that lane (q, row) feeds to the PV MFMA,
-// so each operand is one ds_read_b128. Group gi of row d sits at gi ^ (d >> 4): the
-// 16 rows one fragment read touches share the XOR (conflict-free reads, rows 36 dwords
-// apart), and the 64 transposing writes of a wave (16 dim chunks x key pairs differing
-// in bits 0 and 3) land on distinct banks.
-__device__ __forceinline__ int vt_col(int kp, int dblk) {
-  const int p = kp & 15;
-  const int gi = 4 * (kp >> 4) + ((p & 7) >> 1);
-  return ((gi ^ dblk) << 2) | (2 * (p >> 3) + (p & 1));
-}
+constexpr int kTileRowBytes = kD * 2;  // one key row of one KV head in a tile: 256 B
+constexpr int kTileBytes = kTile * kTileRowBytes;  // 16 KiB
+// Tile layout in LDS. Two K and two V tiles of 64 key rows x 256 B, each its own LDS
+// variable (64 KiB in all). The tiles arrive by direct-to-LDS buffer loads: one wave
+// instruction writes 1 KiB, four whole key rows, so rows cannot be padded; the 16-byte
+// chunks of a row are permuted instead. Chunk c of key row r sits at position
+// c ^ (r & 15) in a K tile, so the 16 rows one QK^T fragment read touches (one chunk
+// each) hit 16 distinct positions, and at c ^ (2 (r & 7)) in a V tile, so the 8 rows x
+// 32 B each half-wave of a transposing P V operand read touches hit 8 distinct 32-byte
+// slots. Both reads are free of bank conflicts. After the tile loop the same 64 KiB
+// stage the output: 8 KiB per wave, its 32 rows of one head at 256 B, chunks placed as in
+// a K tile.
+__device__ __forceinline__ int k_chunk_pos(int r, int c) { return c ^ (r & 15); }
+__device__ __forceinline__ int v_chunk_pos(int r, int c) { return c ^ (2 * (r & 7)); }
 
 // One workgroup per (sequence, block of 256/Gw query rows, group of Gw <= 4 query
 // heads of KV head g). Wave w owns 32 rows (two 16-row MFMA blocks) of head w % Gw.
-// Each 64-key tile of K (row-major) and V (transposed as above) goes through LDS once
-// and feeds all 8 waves; the next tile is prefetched into registers while the current
-// one is consumed. Tiles alternate between two LDS buffers, so one barrier per tile
-// (after the registers are staged) suffices: a buffer is written again two tiles later,
-// after every wave has passed the barrier that follows its last read. Two waves per
-// SIMD hide each other's LDS and memory latency.
+// Each 64-key tile of K and V goes from HBM straight into LDS (no register staging) and
+// feeds all 8 waves: K rows as the QK^T operand, V rows read transposed
+// (ds_read_b64_tr_b16) as the P V operand. The next tile's copies are issued while the
+// current one is consumed; tiles alternate between two LDS buffers, so one wait and one
+// barrier per tile suffice: a buffer is written again two tiles later, after every wave
+// has passed the barrier that follows its last read. The loop body covers two tiles, so
+// every LDS access names its buffer variable statically: the compiler then knows that
+// the copies in flight (into the other buffer) do not alias the reads, and adds no wait
+// for them. Two waves per SIMD hide each other's LDS and memory latency.
 template <typename T, int G>
 __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   typedef hx::Elem<T> E;
   typedef typename E::v8 v8;
   constexpr int Gw = G < 4 ? G : 4;
-  // V^T buffers first: their transposing writes pair up (ds_write2) only with small
-  // offsets.
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kChunkLdsBytes];
-  T* const vt_lds = reinterpret_cast<T*>(lds);                          // two V^T tiles
-  T* const k_lds = reinterpret_cast<T*>(lds + 2 * 2 * kD * kVStride);    // two K tiles
+  __shared__ __attribute__((aligned(16))) uint8_t k_lds0[kTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t k_lds1[kTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t v_lds0[kTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t v_lds1[kTileBytes];
 
   const int tid = hx::tid_x(), lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, held in a scalar register
@@ -1559,14 +1554,6 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   float m_run[2] = {-INFINITY, -INFINITY};  // running row max of the raw scores
   float l_run[2] = {0.f, 0.f};              // this lane's share of the row sum
 
-  const int c16 = tid & 15;     // 16-byte chunk of a key row this thread moves
-  const int kr_base = tid >> 4; // K rows kr_base and kr_base + 32
-  // V rows 2*vkp and 2*vkp + 1 (key pair vkp). Within a wave the four pairs differ in
-  // bits 0 and 3, so the transposing writes below reach all LDS banks.
-  const int vkp = ((tid >> 4) & 1) + 8 * ((tid >> 5) & 1) + 2 * ((tid >> 6) & 3) + 16 * (tid >> 8);
-  // Dword column of key pair vkp in V^T rows d = 8*c16 + 0..7 (see vt_col).
-  const int vcol = vt_col(vkp, c16 >> 1);
-
   // Page ids of the key range, 64 at a time: lane j holds the id of page pg_base + j,
   // so a tile finds its page with one v_readlane instead of a dependent global load.
   const bool paged = a.page_size > 0;
@@ -1582,20 +1569,26 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   // the next tile to load (pages hold a whole number of tiles).
   int ld_pi = pg_base, ld_off = paged ? t_begin * kTile - pg_base * a.page_size : 0;
 
-  // Per-thread byte offsets of the rows this thread loads, relative to the tile's first
-  // row of KV head g (the same for every tile).
+  // Wave w copies key rows 8w..8w+7 of each tile, four rows per instruction: lane l of
+  // copy j moves the 16-byte chunk of row 8w + 4j + l / 16 that belongs at position l % 16
+  // (the permutation above). Its byte offsets from the tile's first row of KV head g are
+  // the same for every tile.
   const uint32_t row_bytes = (uint32_t)a.kv_row * (uint32_t)sizeof(T);
-  const uint32_t koff0 = (uint32_t)kr_base * row_bytes + 16u * (uint32_t)c16, koff1 = koff0 + 32u * row_bytes;
-  const uint32_t voff0 = (uint32_t)(2 * vkp) * row_bytes + 16u * (uint32_t)c16, voff1 = voff0 + row_bytes;
+  uint32_t koffs[2], voffs[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = 8 * w + 4 * j + (lane >> 4), p = lane & 15;
+    koffs[j] = (uint32_t)r * row_bytes + 16u * (uint32_t)k_chunk_pos(r, p);
+    voffs[j] = (uint32_t)r * row_bytes + 16u * (uint32_t)v_chunk_pos(r, p);
+  }
 
   // Each tile's K and V rows are read through buffer resources that end after the tile's
-  // last key (row L - 1 in the last tile): rows past it read zeros, whose scores are
+  // last key (row L - 1 in the last tile): rows past it arrive as zeros, whose scores are
   // masked to -inf (the last tile is never "full"), so no branch or clamp guards the
-  // loads and a tile's addressing is scalar work. A bad page id reads page 0 and is
+  // copies and a tile's addressing is scalar work. A bad page id reads page 0 and is
   // reported in the error word.
-  uint4 kreg[2], vreg[2];
   bool bad_page = false;  // some tile's page id was outside the pool
-  auto load_tile = [&](int t) {
+  auto load_tile = [&](int t, uint8_t* k_dst, uint8_t* v_dst) {
     const int key_base = t * kTile;
     int64_t rowb;
     if (paged) {
@@ -1624,35 +1617,21 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
     const int rows = min(L - key_base, kTile);  // >= 1: key_base <= khi <= L - 1
     const __amdgpu_buffer_rsrc_t kres = hx::buffer_rsrc(kt, (uint32_t)rows * row_bytes);
     const __amdgpu_buffer_rsrc_t vres = hx::buffer_rsrc(vt, (uint32_t)rows * row_bytes);
-    kreg[0] = hx::ld16_buf(kres, koff0);
-    kreg[1] = hx::ld16_buf(kres, koff1);
-    vreg[0] = hx::ld16_buf(vres, voff0);
-    vreg[1] = hx::ld16_buf(vres, voff1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      hx::ld16_to_lds(kres, k_dst + (8 * w + 4 * j) * kTileRowBytes, koffs[j]);
+      hx::ld16_to_lds(vres, v_dst + (8 * w + 4 * j) * kTileRowBytes, voffs[j]);
+    }
   };
 
-  if (t_begin < t_end) load_tile(t_begin);
-  for (int t = t_begin; t < t_end; ++t) {
-    const int hb = (t - t_begin) & 1;
-    T* const kl = k_lds + hb * (kTile * kKStride);
-    T* const vl = vt_lds + hb * (kD * kVStride);
-    // Registers -> LDS: K row-major, V transposed (pairs of keys packed per 32-bit word).
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      *reinterpret_cast<uint4*>(&kl[(kr_base + 32 * j) * kKStride + 8 * c16]) = kreg[j];
-    {
-      const uint4 x = vreg[0], y = vreg[1];
-      const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
-      const uint32_t ys[4] = {y.x, y.y, y.z, y.w};
-      uint32_t* vt32 = reinterpret_cast<uint32_t*>(vl);
-#pragma unroll
-      for (int wd = 0; wd < 4; ++wd) {
-        const int d = 8 * c16 + 2 * wd;
-        vt32[d * (kVStride / 2) + vcol] = hx::interleave_lo(xs[wd], ys[wd]);
-        vt32[(d + 1) * (kVStride / 2) + vcol] = hx::interleave_hi(xs[wd], ys[wd]);
-      }
-    }
+  // Tile t (in buffers kl, vl): wait for it, start tile t + 1 into (kn, vn), consume t.
+  auto tile_step = [&](int t, const uint8_t* kl, const uint8_t* vl, uint8_t* kn, uint8_t* vn)
+                       __attribute__((always_inline)) {
+    // This wave's copies of tile t have landed; after the barrier, every wave's have, and
+    // every wave is done with tile t - 1, whose buffers tile t + 1 now fills.
+    __builtin_amdgcn_s_waitcnt(hx::kWaitVm0);
     __syncthreads();
-    if (t + 1 < t_end) load_tile(t + 1);
+    if (t + 1 < t_end) load_tile(t + 1, kn, vn);
 
     const int t0 = t * kTile;
     // S^T = K Q^T: lane holds keys 16kb+4(lane>>4)+i of row 16rb+(lane&15).
@@ -1665,8 +1644,9 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
     for (int st = 0; st < 4; ++st) {
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
+        const int kr = 16 * kb + (lane & 15);
         const uint4 af = *reinterpret_cast<const uint4*>(
-            &kl[(16 * kb + (lane & 15)) * kKStride + 32 * st + 8 * (lane >> 4)]);
+            kl + kr * kTileRowBytes + 16 * k_chunk_pos(kr, 4 * st + (lane >> 4)));
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
           sacc[kb][rb] = E::mfma16x16x32(hx::as_v8<T>(af), hx::as_v8<T>(qf[rb][st]), sacc[kb][rb]);
@@ -1758,17 +1738,35 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
     // O^T += V^T P^T with the key order of pb: {4(lane>>4)+0..3, 16+4(lane>>4)+0..3}.
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
+      // V^T operand of dim block db: lane (g, j) = (lane / 16, lane % 16) needs dim
+      // 16 db + j of keys 32 ks + 4g + 0..3 and 32 ks + 16 + 4g + 0..3 (the key order of
+      // pb). Each transposing read gives a 16-lane group the 4 x 16 block of 4 key rows
+      // x 16 dims its lanes address (lane i: row i / 4, dims 4 (i % 4)..+3), lane j taking
+      // column j.
       uint4 vf[8];  // all eight dim blocks of this key step, read before their MFMAs
+      {
+        const int g = lane >> 4, i = lane & 15;
+        const int r0 = 32 * ks + 4 * g + (i >> 2), r1 = r0 + 16;
 #pragma unroll
-      for (int db = 0; db < 8; ++db)
-        vf[db] = *reinterpret_cast<const uint4*>(
-            &vl[(16 * db + (lane & 15)) * kVStride + 8 * ((4 * ks + (lane >> 4)) ^ db)]);
+        for (int db = 0; db < 8; ++db) {
+          const int c = 2 * db + ((i >> 1) & 1);
+          const uint2 lo = hx::ld8_lds_tr16(vl + r0 * kTileRowBytes + 16 * v_chunk_pos(r0, c) + 8 * (i & 1));
+          const uint2 hi = hx::ld8_lds_tr16(vl + r1 * kTileRowBytes + 16 * v_chunk_pos(r1, c) + 8 * (i & 1));
+          vf[db] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        }
+      }
 #pragma unroll
       for (int db = 0; db < 8; ++db)
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
           oacc[db][rb] = E::mfma16x16x32(hx::as_v8<T>(vf[db]), pb[ks][rb], oacc[db][rb]);
     }
+  };
+
+  if (t_begin < t_end) load_tile(t_begin, k_lds0, v_lds0);
+  for (int t = t_begin; t < t_end; t += 2) {
+    tile_step(t, k_lds0, v_lds0, k_lds1, v_lds1);
+    if (t + 1 < t_end) tile_step(t + 1, k_lds1, v_lds1, k_lds0, v_lds0);
   }
 
   if (bad_page && tid == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_BAD_PAGE);
@@ -1779,16 +1777,17 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   // 16 rows per instruction, about 2.5 us more per workgroup). A split writes its
   // partial (m in log2 units, l, o / l) to the row's slot instead of the output.
   const int64_t slot0 = S > 1 ? a.dec_cap + a.pf_base[item] + sp : 0;
-  uint8_t* const stage = lds + w * (32 * kStageStride);
+  uint8_t* const stage = (w < 4 ? (w < 2 ? k_lds0 : k_lds1) : (w < 6 ? v_lds0 : v_lds1)) + (w & 1) * (32 * kTileRowBytes);
   __syncthreads();  // every wave is done with the tiles
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
     const float l = hx::add_xor32(hx::add_xor16(l_run[rb]));
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    uint8_t* srow = stage + (16 * rb + (lane & 15)) * kStageStride + 8 * (lane >> 4);
+    const int sr = 16 * rb + (lane & 15);
+    uint8_t* const srow = stage + sr * kTileRowBytes + 8 * ((lane >> 4) & 1);
 #pragma unroll
     for (int db = 0; db < 8; ++db)
-      *reinterpret_cast<uint2*>(srow + 32 * db) =
+      *reinterpret_cast<uint2*>(srow + 16 * k_chunk_pos(sr, 2 * db + (lane >> 5))) =
           make_uint2(hx::pack2_round<T>(oacc[db][rb][0] * inv, oacc[db][rb][1] * inv),
                      hx::pack2_round<T>(oacc[db][rb][2] * inv, oacc[db][rb][3] * inv));
     const int rr = wr0 + 16 * rb + (lane & 15);
@@ -1810,7 +1809,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   for (int i = 0; i < 8; ++i) {
     const int sr = 4 * i + (lane >> 4);
     const int rr = wr0 + sr;
-    const uint4 u = *reinterpret_cast<const uint4*>(stage + sr * kStageStride + 16 * (lane & 15));
+    const uint4 u = *reinterpret_cast<const uint4*>(stage + sr * kTileRowBytes + 16 * k_chunk_pos(sr, lane & 15));
     if (rr >= n) continue;
     if (S > 1) {
       const int64_t slot = slot0 + (int64_t)(rr - row0) * S;
