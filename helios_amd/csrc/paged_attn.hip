@@ -1624,6 +1624,23 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
     }
   };
 
+  // V^T operands of key step ks (keys 32 ks .. 32 ks + 31) of a V tile, dim block db in
+  // vf[db]: lane (g, j) = (lane / 16, lane % 16) needs dim 16 db + j of keys 32 ks + 4g
+  // + 0..3 and 32 ks + 16 + 4g + 0..3 (the key order of the P operand). Each transposing
+  // read gives a 16-lane group the 4 x 16 block of 4 key rows x 16 dims its lanes address
+  // (lane i: row i / 4, dims 4 (i % 4)..+3), lane j taking column j.
+  auto read_v = [&](const uint8_t* vl, int ks, uint4 (&vf)[8]) __attribute__((always_inline)) {
+    const int gg = lane >> 4, i = lane & 15;
+    const int r0 = 32 * ks + 4 * gg + (i >> 2), r1 = r0 + 16;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const int c = 2 * db + ((i >> 1) & 1);
+      const uint2 lo = hx::ld8_lds_tr16(vl + r0 * kTileRowBytes + 16 * v_chunk_pos(r0, c) + 8 * (i & 1));
+      const uint2 hi = hx::ld8_lds_tr16(vl + r1 * kTileRowBytes + 16 * v_chunk_pos(r1, c) + 8 * (i & 1));
+      vf[db] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
+  };
+
   // Tile t (in buffers kl, vl): wait for it, start tile t + 1 into (kn, vn), consume t.
   auto tile_step = [&](int t, const uint8_t* kl, const uint8_t* vl, uint8_t* kn, uint8_t* vn)
                        __attribute__((always_inline)) {
@@ -1652,6 +1669,10 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
           sacc[kb][rb] = E::mfma16x16x32(hx::as_v8<T>(af), hx::as_v8<T>(qf[rb][st]), sacc[kb][rb]);
       }
     }
+
+    // V operands of the first P V key step, in flight during the softmax.
+    uint4 vf0[8];
+    read_v(vl, 0, vf0);
 
     // Mask only where the tile is not fully visible to every row of this wave (a
     // wave-uniform test, evaluated on the scalar unit).
@@ -1736,31 +1757,19 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
     }
 
     // O^T += V^T P^T with the key order of pb: {4(lane>>4)+0..3, 16+4(lane>>4)+0..3}.
+    // The first key step's V operands were read before the softmax.
+    uint4 vf1[8];
+    read_v(vl, 1, vf1);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      // V^T operand of dim block db: lane (g, j) = (lane / 16, lane % 16) needs dim
-      // 16 db + j of keys 32 ks + 4g + 0..3 and 32 ks + 16 + 4g + 0..3 (the key order of
-      // pb). Each transposing read gives a 16-lane group the 4 x 16 block of 4 key rows
-      // x 16 dims its lanes address (lane i: row i / 4, dims 4 (i % 4)..+3), lane j taking
-      // column j.
-      uint4 vf[8];  // all eight dim blocks of this key step, read before their MFMAs
-      {
-        const int g = lane >> 4, i = lane & 15;
-        const int r0 = 32 * ks + 4 * g + (i >> 2), r1 = r0 + 16;
+    for (int db = 0; db < 8; ++db)
 #pragma unroll
-        for (int db = 0; db < 8; ++db) {
-          const int c = 2 * db + ((i >> 1) & 1);
-          const uint2 lo = hx::ld8_lds_tr16(vl + r0 * kTileRowBytes + 16 * v_chunk_pos(r0, c) + 8 * (i & 1));
-          const uint2 hi = hx::ld8_lds_tr16(vl + r1 * kTileRowBytes + 16 * v_chunk_pos(r1, c) + 8 * (i & 1));
-          vf[db] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        }
-      }
+      for (int rb = 0; rb < 2; ++rb)
+        oacc[db][rb] = E::mfma16x16x32(hx::as_v8<T>(vf0[db]), pb[0][rb], oacc[db][rb]);
 #pragma unroll
-      for (int db = 0; db < 8; ++db)
+    for (int db = 0; db < 8; ++db)
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-          oacc[db][rb] = E::mfma16x16x32(hx::as_v8<T>(vf[db]), pb[ks][rb], oacc[db][rb]);
-    }
+      for (int rb = 0; rb < 2; ++rb)
+        oacc[db][rb] = E::mfma16x16x32(hx::as_v8<T>(vf1[db]), pb[1][rb], oacc[db][rb]);
   };
 
   if (t_begin < t_end) load_tile(t_begin, k_lds0, v_lds0);
