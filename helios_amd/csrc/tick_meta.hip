@@ -205,7 +205,7 @@ __global__ __launch_bounds__(256) void merge_kernel(uint16_t* out, int64_t o_row
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const float xa = (float)__builtin_bit_cast(T, pa[lane + 64 * k]);
-      acc[k] = (xa * wa + acc[k] * wb) / (wa + wb);
+      acc[k] = fmaf(xa, wa, acc[k] * wb) / (wa + wb);  // one rounding order in both kernels
     }
     m = mn + logf(wa + wb);
     changed = true;
@@ -214,6 +214,89 @@ __global__ __launch_bounds__(256) void merge_kernel(uint16_t* out, int64_t o_row
 #pragma unroll
   for (int k = 0; k < 2; ++k) po[lane + 64 * k] = __builtin_bit_cast(uint16_t, (T)acc[k]);
   if (lane == 0) *lb_p = m;
+}
+
+// merge_kernel's arithmetic with a short dependency chain: 16 lanes per (entry j, head h),
+// lane i owning dims 8i..8i+7 (16-byte loads; rows 16-byte aligned, checked on the host),
+// and the part indices, part log-sum-exps and part rows of up to four parts loaded
+// together before they are folded, in list order, exactly as merge_kernel folds them.
+template <typename T>
+__global__ __launch_bounds__(256) void merge_vec_kernel(uint16_t* out, int64_t o_row, int64_t o_head,
+                                                        float* lse_out, int64_t total_out,
+                                                        const uint16_t* oa, int64_t a_row, int64_t a_head,
+                                                        const float* lse_a, int64_t total_a,
+                                                        const int64_t* rows, const int32_t* part_start,
+                                                        const int32_t* part_idx, int64_t n_parts,
+                                                        int64_t n_rows, int hq) {
+  const int64_t item = (int64_t)hx::wg_x() * 16 + (hx::tid_x() >> 4);
+  const int li = hx::tid_x() & 15;
+  if (item >= n_rows * hq) return;
+  const int64_t j = item / hq;
+  const int h = (int)(item - j * hq);
+  const int64_t r = rows[j];
+  int64_t p0 = j, p1 = j + 1;
+  if (part_start != nullptr) {  // a range outside the part list is clipped to it
+    p0 = max((int64_t)part_start[j], (int64_t)0);
+    p1 = min((int64_t)part_start[j + 1], n_parts);
+  }
+  if (r < 0 || r >= total_out) return;
+  float* lb_p = lse_out + (int64_t)h * total_out + r;
+  uint16_t* po = out + r * o_row + (int64_t)h * o_head + 8 * li;
+  float m = *lb_p;  // the running result is normalised, with log-sum-exp m
+  const uint4 ov = *reinterpret_cast<const uint4*>(po);
+  float acc[8];
+  {
+    const uint32_t w4[4] = {ov.x, ov.y, ov.z, ov.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[2 * e] = hx::Elem<T>::lo(w4[e]);
+      acc[2 * e + 1] = hx::Elem<T>::hi(w4[e]);
+    }
+  }
+  bool changed = false;
+  for (int64_t pb = p0; pb < p1; pb += 4) {
+    int64_t ja[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      ja[k] = -1;
+      if (pb + k < p1) ja[k] = part_start != nullptr ? (int64_t)part_idx[pb + k] : pb + k;
+    }
+    float la[4];
+    uint4 pv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const bool ok = ja[k] >= 0 && ja[k] < total_a;
+      la[k] = ok ? lse_a[(int64_t)h * total_a + ja[k]] : -INFINITY;
+      pv[k] = ok ? *reinterpret_cast<const uint4*>(oa + ja[k] * a_row + (int64_t)h * a_head + 8 * li)
+                 : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (!(ja[k] >= 0 && ja[k] < total_a)) continue;
+      const float mn = fmaxf(m, la[k]);
+      if (mn == -INFINITY) continue;  // neither side saw a key yet
+      const float wa = expf(la[k] - mn), wb = expf(m - mn);
+      const uint32_t w4[4] = {pv[k].x, pv[k].y, pv[k].z, pv[k].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float xa0 = hx::Elem<T>::lo(w4[e]), xa1 = hx::Elem<T>::hi(w4[e]);
+        acc[2 * e] = fmaf(xa0, wa, acc[2 * e] * wb) / (wa + wb);
+        acc[2 * e + 1] = fmaf(xa1, wa, acc[2 * e + 1] * wb) / (wa + wb);
+      }
+      m = mn + logf(wa + wb);
+      changed = true;
+    }
+  }
+  if (!changed) return;
+  uint4 u;
+  u.x = hx::pack2_round<T>(acc[0], acc[1]);
+  u.y = hx::pack2_round<T>(acc[2], acc[3]);
+  u.z = hx::pack2_round<T>(acc[4], acc[5]);
+  u.w = hx::pack2_round<T>(acc[6], acc[7]);
+  // Every lane of the entry has read the old lse (above, before any fold) before lane 0
+  // of the entry stores the merged one: all 16 lanes sit in one wave, in program order.
+  *reinterpret_cast<uint4*>(po) = u;
+  if (li == 0) *lb_p = m;
 }
 
 }  // namespace
@@ -237,6 +320,21 @@ extern "C" int hx_attn_merge(void* out, int64_t out_row_stride, int64_t out_head
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   uint16_t* o = static_cast<uint16_t*>(out);
   const uint16_t* a = static_cast<const uint16_t*>(o_a);
+  const bool vec = out_row_stride % 8 == 0 && out_head_stride % 8 == 0 && a_row_stride % 8 == 0 &&
+                   a_head_stride % 8 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(o_a) % 16 == 0;
+  if (vec) {
+    const unsigned vgrid = (unsigned)((items + 15) / 16);
+    if (dtype == HX_DTYPE_BF16)
+      hipLaunchKernelGGL(merge_vec_kernel<__bf16>, dim3(vgrid), dim3(256), 0, s, o, out_row_stride,
+                         out_head_stride, lse_out, total_out, a, a_row_stride, a_head_stride, lse_a, total_a,
+                         rows, part_start, part_idx, n_parts, n_rows, n_heads);
+    else
+      hipLaunchKernelGGL(merge_vec_kernel<_Float16>, dim3(vgrid), dim3(256), 0, s, o, out_row_stride,
+                         out_head_stride, lse_out, total_out, a, a_row_stride, a_head_stride, lse_a, total_a,
+                         rows, part_start, part_idx, n_parts, n_rows, n_heads);
+    return hx::status_from_hip(hipGetLastError());
+  }
   if (dtype == HX_DTYPE_BF16)
     hipLaunchKernelGGL(merge_kernel<__bf16>, dim3(grid), dim3(256), 0, s, o, out_row_stride, out_head_stride,
                        lse_out, total_out, a, a_row_stride, a_head_stride, lse_a, total_a, rows, part_start,

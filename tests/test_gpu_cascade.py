@@ -242,6 +242,48 @@ def test_attn_merge_folds_several_parts(device):
         assert torch.equal(out_d[r].cpu(), out[r].to(torch.bfloat16))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_attn_merge_vector_and_scalar_paths_agree(device, dtype):
+    """The 16-byte merge (16-byte aligned rows) and the 2-byte one (other strides) give the
+    same bits, with up to 7 parts per row (more than one batch of four) and parts whose
+    log-sum-exp is -inf."""
+    say(f"attn merge paths {dtype}")
+    g = torch.Generator(device="cpu").manual_seed(2)
+    heads, d, rows, n_a = 4, 128, 5, 16
+    out = torch.randn(rows, heads, d, generator=g)
+    lse_out = torch.randn(heads, rows, generator=g)
+    lse_out[:, 4] = -float("inf")
+    o_a = torch.randn(n_a, heads, d, generator=g)
+    lse_a = torch.randn(heads, n_a, generator=g) * 3
+    lse_a[:, 5] = -float("inf")
+    members = {0: [0, 1, 2, 3, 4, 5, 6], 2: [7, 8], 3: [9], 4: [10, 5, 11, 12, 13]}
+    out_rows = sorted(members)
+    part_start, part_idx = [0], []
+    for r in out_rows:
+        part_idx += members[r]
+        part_start.append(len(part_idx))
+    parts = (torch.tensor(part_start, dtype=torch.int32, device=device),
+             torch.tensor(part_idx, dtype=torch.int32, device=device))
+    rows_d = torch.tensor(out_rows, device=device)
+    a_d = o_a.to(dtype).to(device)
+    la_d = lse_a.contiguous().to(device)
+
+    def run(out_t):
+        lse_t = lse_out.clone().contiguous().to(device)
+        ops.attn_merge(out_t, lse_t, a_d, la_d, rows_d, parts=parts)
+        return out_t, lse_t
+
+    vec_out, vec_lse = run(out.to(dtype).to(device))
+    wide = torch.zeros(rows, heads, d + 4, dtype=dtype, device=device)
+    wide[:, :, :d] = out.to(dtype).to(device)
+    sc_out, sc_lse = run(wide[:, :, :d])  # head stride 132: not 16-byte aligned
+    assert sc_out.stride(1) % 8 != 0
+    torch.cuda.synchronize()
+    assert torch.equal(vec_out.cpu(), sc_out.cpu())
+    assert torch.equal(vec_lse.cpu(), sc_lse.cpu())
+    assert torch.equal(vec_out[1].cpu(), out[1].to(dtype))  # not a member: untouched
+
+
 @pytest.mark.parametrize("cascade", [True, False])
 def test_overlapped_streams_give_the_same_bits(device, cascade, always_cascade):
     """Chunk rows and the cascade's batch A on a second stream, decode rows on the
