@@ -362,11 +362,13 @@ def long_context(device, steps: int = 10, warmup: int = 3):
     chunk_us = chunk_kernel_us + combine_us
     del b
     torch.cuda.empty_cache()
-    # restore copy: 16 prefix pages of every layer, keys and values
+    # restore copy: 16 prefix pages of every layer, keys and values, in the pool layout
+    # KVPagePool allocates (one [2, layers, pages, ...] tensor, per-layer views)
     layers, n = N_LAYERS_MODEL, 16
-    shape = (2 * n, w.page_size, w.n_kv_heads, w.head_dim)
-    kl = [torch.randn(shape, device=device, dtype=torch.bfloat16) for _ in range(layers)]
-    vl = [torch.randn(shape, device=device, dtype=torch.bfloat16) for _ in range(layers)]
+    store = torch.randn((2, layers, 2 * n, w.page_size, w.n_kv_heads, w.head_dim), device=device,
+                        dtype=torch.bfloat16)
+    kl = [store[0, layer] for layer in range(layers)]
+    vl = [store[1, layer] for layer in range(layers)]
     src, dst = list(range(n)), list(range(n, 2 * n))
     for _ in range(3):
         ops.kv_copy_pages(kl, vl, src, dst)
@@ -378,10 +380,10 @@ def long_context(device, steps: int = 10, warmup: int = 3):
     torch.cuda.synchronize()
     copy_us = statistics.median(a_.elapsed_time(b_) for a_, b_ in cev) * 1e3
     copy_bytes = 2 * layers * 2 * n * kl[0][0].numel() * 2
-    # every copied page of every layer, K and V, bit for bit (72 tensors: two launches)
+    # every copied page of every layer, K and V, bit for bit (72 tensors, one launch)
     for t in kl + vl:
         assert torch.equal(t[dst].view(torch.int16), t[src].view(torch.int16)), "restore copy differs"
-    del kl, vl
+    del kl, vl, store
     torch.cuda.empty_cache()
     # page gather (_gather_cpu's paged -> dense [1, 8, L, 128]) of one 32768-key sequence
     pool = torch.randn((160, w.page_size, w.n_kv_heads, w.head_dim), device=device, dtype=torch.bfloat16)

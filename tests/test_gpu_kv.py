@@ -169,9 +169,10 @@ def test_gather_narrow_rows_take_the_generic_path(device, dtype, heads, dim):
 def test_c4_restore_of_16_prefix_pages_over_36_layers(device):
     """The C4 restore at its full size, through the pool: a request restores a 16-page
     prefix snapshot with ``restore_blocks(copy=True)``, which copies those pages for all
-    36 layers, K and V (72 tensors of [pages, 256, 8, 128] bf16, more than one launch
-    takes). Every destination page equals its source bit for bit, as torch's copy_ of
-    the same pages gives, and no other page changes."""
+    36 layers, K and V (72 tensors of [pages, 256, 8, 128] bf16, more than a launch's
+    tensor table holds; the pool's constant layer stride lets one launch cover them).
+    Every destination page equals its source bit for bit, as torch's copy_ of the same
+    pages gives, and no other page changes."""
     from helios_amd.config import Qwen3Config
     from helios_amd.paged_cache import KVPagePool, PagedKVCache
 
