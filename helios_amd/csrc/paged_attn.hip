@@ -55,9 +55,12 @@ constexpr int kPlanThreads = 1024;
 // split count per block spills past whole rounds, the split size grows to the smallest
 // one that fits them (refine_split_tiles). On the full-model tick this took the 1024-row
 // chunk from about 550 workgroups (a third, partial round) to 512: 143 -> 110 us.
+// Pieces of 4 tiles: the full-model tick's shared-prefix levels (4 sequences of 69-128
+// rows over 3-5 pages) then run in 256 workgroups instead of 144 (chunk 24.5 -> 17.1 us,
+// with its combine 32.7 -> 29.2 us); chunks of 2016 rows and more plan as with 8.
 constexpr int kChunkFillWGs = 512;
 constexpr int kChunkCUs = 256;  // CUs of an MI355X
-constexpr int kMinSplitTiles = 8;
+constexpr int kMinSplitTiles = 4;
 constexpr int kMaxChunkSplits = 64;
 constexpr int kCombRows = 8;  // output rows per combine record of a split chunk block
 constexpr int kAppendWGs = 256;  // append workgroups in a decode launch, at most

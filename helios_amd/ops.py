@@ -58,7 +58,9 @@ class AuxRequest(NamedTuple):
 
 
 def _stream_ptr(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The current stream's handle on ``device`` (the raw lookup: no Stream object)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
 def _require_gpu(*tensors: torch.Tensor) -> torch.device:

@@ -13,7 +13,7 @@ workspace. This module builds the same lists from the host lengths:
 Sequences go in order and a chunk's row blocks from the last to the first. When the tick
 has at most 256 row blocks, the chunk items are then reordered block by block, longest
 first: by key tiles per item, descending, ties in that order. The split size
-follows the documented rule (at least max(8, ceil(tiles * Hkv / 512)) tiles when the
+follows the documented rule (at least max(4, ceil(tiles * Hkv / 512)) tiles when the
 unsplit chunk items launch fewer than 512 workgroups, raised to the smallest size that
 fits whole rounds of 256 workgroups, or one round when the size that fits one round is
 at most 1.25 x the chunk tiles per CU); then only blocks longer than max(split size,
@@ -28,7 +28,7 @@ SPLIT = 256
 TILE = 64
 FILL_WGS = 512
 CUS = 256
-MIN_SPLIT_TILES = 8
+MIN_SPLIT_TILES = 4
 MAX_SPLITS = 64
 COMB_ROWS = 8
 SORT_BLOCKS = 256  # ticks of at most this many row blocks list chunk items longest first

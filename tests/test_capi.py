@@ -58,7 +58,7 @@ def test_workspace_bytes_supported_shapes():
 def _expected_counts(w: synth.Workload, window=(-1, 0)):
     """Work items from the closed forms: decode rows split keys in 256s; chunk rows go in
     blocks of rows_per_item, and when the unsplit blocks launch fewer than 512 workgroups
-    each block's 64-key tiles are cut into splits of at least max(8, ceil(tiles * Hkv /
+    each block's 64-key tiles are cut into splits of at least max(4, ceil(tiles * Hkv /
     512)) tiles, every split row adding one combine record. When the split workgroups
     spill past R >= 1 whole rounds of 256 (one chunk workgroup per CU), the split size is
     the smallest one, up to the largest block's tiles, whose count fits R rounds, or one
@@ -82,7 +82,7 @@ def _expected_counts(w: synth.Workload, window=(-1, 0)):
     tiles0 = sum(tiles(*blk) for blk in blocks) * quads
     split = 0
     if items0 and items0 * w.n_kv_heads < 512:
-        split = max(8, -(-tiles0 * w.n_kv_heads // 512))
+        split = max(4, -(-tiles0 * w.n_kv_heads // 512))
 
     def split_count(t, st, keep=None):
         keep = st if keep is None else keep

@@ -66,3 +66,15 @@ def test_generic_shape_overlapped_matches_run(device):
     torch.cuda.synchronize()
     assert plan.error_word() == 0
     assert torch.equal(got, ref)
+
+
+def test_stream_handle_is_the_current_stream(device):
+    """Launches go to torch's current stream: the raw handle lookup agrees with
+    ``torch.cuda.current_stream`` on the default stream, under ``torch.cuda.stream`` and
+    for a device given without an index."""
+    side = torch.cuda.Stream(device=device)
+    assert ops._stream_ptr(device) == torch.cuda.current_stream(device).cuda_stream
+    with torch.cuda.stream(side):
+        assert ops._stream_ptr(device) == side.cuda_stream
+        assert ops._stream_ptr(torch.device("cuda")) == side.cuda_stream
+    assert ops._stream_ptr(device) == torch.cuda.current_stream(device).cuda_stream
