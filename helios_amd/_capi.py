@@ -13,7 +13,7 @@ HEADER_PATH = Path(__file__).resolve().parent.parent / "include" / "helios_paged
 
 HX_OK = 0
 # hx_abi_version() of the library these signatures describe (bumped on any signature change).
-ABI_VERSION = 3
+ABI_VERSION = 4
 HX_E_INVALID_ARG = -1
 HX_E_UNSUPPORTED = -2
 HX_E_WORKSPACE = -3
@@ -28,6 +28,7 @@ HX_WERR_CLAMPED_LEN = 2
 HX_WERR_BAD_CU_SEQ = 4
 HX_WERR_GRID = 8
 HX_WERR_PLAN_MISMATCH = 16
+HX_WERR_BAD_QUERY_ROW = 32
 
 _c_void_p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -74,6 +75,19 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "hx_varlen_attn_run": (
         ctypes.c_int,
         [_c_void_p, _i64, _i64,
+         _c_void_p, _c_void_p, _i64, _i64,
+         _i32, _i32, _c_void_p, _i32,
+         _i32, _i32, _i32, _i32,
+         _i32, _i32, _i32,
+         _f32, _i32, _i32, _i32,
+         _c_void_p, _i64, _i64, _c_void_p,
+         _i32, _i32, _i32,
+         _c_void_p, _size, _c_void_p],
+    ),
+    "hx_varlen_attn_run_rows": (
+        ctypes.c_int,
+        [_c_void_p, _i64, _i64,
+         _c_void_p, _i64,
          _c_void_p, _c_void_p, _i64, _i64,
          _i32, _i32, _c_void_p, _i32,
          _i32, _i32, _i32, _i32,

@@ -896,7 +896,21 @@ struct RunArgs {
   // Workgroups after the decode workgroups of the decode launch that append every row of
   // the tick (0: none; the chunk rows then went in by a separate append beforehand).
   int32_t app_wgs;
+  // Query row of each packed row (nullptr: the packed row itself); q holds q_rows_total
+  // rows when the map is given.
+  const int64_t* q_rows;
+  int64_t q_rows_total;
 };
+
+// Row of q that packed row r reads. A map entry outside the query tensor reads row 0 and
+// is reported in the error word.
+__device__ __forceinline__ int64_t query_row(const RunArgs& a, int64_t r) {
+  if (a.q_rows == nullptr) return r;
+  const int64_t m = a.q_rows[r];
+  if ((uint64_t)m < (uint64_t)a.q_rows_total) return m;
+  atomicOr(&a.hdr[H_ERR], HX_WERR_BAD_QUERY_ROW);
+  return 0;
+}
 
 // True when the workspace holds a plan for this run's shape; otherwise the block
 // raises HX_WERR_PLAN_MISMATCH (once) and the caller must return without touching
@@ -1105,7 +1119,7 @@ __global__ __launch_bounds__(kThreads, (decode_min_wgs<T, G>())) void decode_ker
   const int r = lane >> 4, c = lane & 15;
   uint4 qf[G];
   {
-    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)q0 * a.q_row + (int64_t)(g * G) * a.q_head + 8 * c;
+    const T* qp = reinterpret_cast<const T*>(a.q) + query_row(a, q0) * a.q_row + (int64_t)(g * G) * a.q_head + 8 * c;
 #pragma unroll
     for (int h = 0; h < G; ++h) qf[h] = ld16(qp + (int64_t)h * a.q_head);
   }
@@ -1543,7 +1557,7 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   for (int rb = 0; rb < 2; ++rb) {
     const int rr = wr0 + 16 * rb + (lane & 15);
     const bool ok = rr < n;
-    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)(q0 + (ok ? rr : 0)) * a.q_row +
+    const T* qp = reinterpret_cast<const T*>(a.q) + query_row(a, q0 + (ok ? rr : 0)) * a.q_row +
                   (int64_t)qh * a.q_head + 8 * (lane >> 4);
 #pragma unroll
     for (int st = 0; st < 4; ++st) qf[rb][st] = ok ? ld16(qp + 32 * st) : hx::zero4();
@@ -1899,7 +1913,7 @@ __global__ __launch_bounds__(256) void generic_kernel(RunArgs a, GenericShape gs
   // The units' queries, widened to fp32.
   for (int idx = tid; idx < units * D; idx += 256) {
     const int u = idx / D, d = idx - (idx / D) * D;
-    const int64_t qrow = q0 + row0 + u / hcount;
+    const int64_t qrow = query_row(a, q0 + row0 + u / hcount);
     const int qh = g * gs.group + h0 + u % hcount;
     q_lds[u * DMAX + d] = E::lo(reinterpret_cast<const uint16_t*>(a.q)[qrow * a.q_row + (int64_t)qh * a.q_head + d]);
   }
@@ -2218,6 +2232,7 @@ struct AppendSpec {
 };
 
 int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+             const int64_t* q_rows, int64_t q_rows_total,
              const void* k_cache, const void* v_cache,
              int64_t kv_row_stride, int64_t kv_head_stride,
              int32_t num_pages, int32_t page_size,
@@ -2303,6 +2318,8 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
   a.kn_row = a.kn_head = a.vn_row = a.vn_head = 0;
   a.pool_rows = 0;
   a.app_wgs = 0;
+  a.q_rows = q_rows;
+  a.q_rows_total = q_rows_total;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int G = n_q_heads / n_kv_heads;
   const bool tuned = tuned_shape(G, head_dim);
@@ -2377,11 +2394,35 @@ int hx_varlen_attn_run(const void* q, int64_t q_row_stride, int64_t q_head_strid
                        int32_t decode_items_hint, int32_t prefill_items_hint,
                        int32_t combine_seqs_hint,
                        void* workspace, size_t workspace_bytes, void* stream) {
-  return run_impl(q, q_row_stride, q_head_stride, k_cache, v_cache, kv_row_stride, kv_head_stride,
+  return run_impl(q, q_row_stride, q_head_stride, nullptr, 0, k_cache, v_cache, kv_row_stride, kv_head_stride,
                   num_pages, page_size, block_table, block_table_stride, batch, total_q, max_q,
                   max_k, n_q_heads, n_kv_heads, head_dim, scale, window_left, window_right, dtype,
                   out, o_row_stride, o_head_stride, lse, decode_items_hint, prefill_items_hint,
                   combine_seqs_hint, workspace, workspace_bytes, stream, nullptr);
+}
+
+int hx_varlen_attn_run_rows(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                            const int64_t* query_rows, int64_t query_rows_total,
+                            const void* k_cache, const void* v_cache,
+                            int64_t kv_row_stride, int64_t kv_head_stride,
+                            int32_t num_pages, int32_t page_size,
+                            const int32_t* block_table, int32_t block_table_stride,
+                            int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                            int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                            float scale, int32_t window_left, int32_t window_right,
+                            int32_t dtype,
+                            void* out, int64_t o_row_stride, int64_t o_head_stride,
+                            float* lse,
+                            int32_t decode_items_hint, int32_t prefill_items_hint,
+                            int32_t combine_seqs_hint,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  if (total_q > 0 && batch > 0 && (!query_rows || query_rows_total < 1)) return HX_E_INVALID_ARG;
+  return run_impl(q, q_row_stride, q_head_stride, query_rows, query_rows_total, k_cache, v_cache,
+                  kv_row_stride, kv_head_stride, num_pages, page_size, block_table,
+                  block_table_stride, batch, total_q, max_q, max_k, n_q_heads, n_kv_heads, head_dim,
+                  scale, window_left, window_right, dtype, out, o_row_stride, o_head_stride, lse,
+                  decode_items_hint, prefill_items_hint, combine_seqs_hint, workspace,
+                  workspace_bytes, stream, nullptr);
 }
 
 int hx_varlen_attn_append_run(const void* q, int64_t q_row_stride, int64_t q_head_stride,
@@ -2410,7 +2451,7 @@ int hx_varlen_attn_append_run(const void* q, int64_t q_row_stride, int64_t q_hea
   app.vn_head = v_new_head_stride;
   app.write_slots = write_slots;
   app.pool_rows = pool_rows;
-  return run_impl(q, q_row_stride, q_head_stride, k_cache, v_cache, kv_row_stride, kv_head_stride,
+  return run_impl(q, q_row_stride, q_head_stride, nullptr, 0, k_cache, v_cache, kv_row_stride, kv_head_stride,
                   num_pages, page_size, block_table, block_table_stride, batch, total_q, max_q,
                   max_k, n_q_heads, n_kv_heads, head_dim, scale, window_left, window_right, dtype,
                   out, o_row_stride, o_head_stride, lse, decode_items_hint, prefill_items_hint,

@@ -42,6 +42,7 @@ _WERR_TEXT = {
     _capi.HX_WERR_BAD_CU_SEQ: "cu_seq_q not monotone or beyond the query rows",
     _capi.HX_WERR_GRID: "more work items than the launch grid covered",
     _capi.HX_WERR_PLAN_MISMATCH: "a run whose shape differs from its plan",
+    _capi.HX_WERR_BAD_QUERY_ROW: "a query row map entry outside the query tensor",
 }
 
 
@@ -585,6 +586,7 @@ class VarlenAttnPlan:
         lse_out: torch.Tensor | None = None,
         phases: tuple[str, ...] = ("decode", "chunk", "combine"),
         append: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
+        query_rows: torch.Tensor | None = None,
     ) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
         """Attention for one layer. ``phases`` launches a subset of the three kernels
         (decode splits, chunk rows, split combine); a full result needs all three, with
@@ -596,6 +598,13 @@ class VarlenAttnPlan:
         ``append=(k_new, v_new, write_slots)`` first writes the tick's new K/V rows
         into the pool (index_copy_ semantics, as ``kv_append``) in the same call: decode
         rows inside the decode kernel, chunk rows by the append kernel beforehand.
+
+        ``query_rows`` (int64 ``[total_q]`` on the device) reads packed row t's query
+        from ``query[query_rows[t]]``, so ``query`` may be any ``[N, n_q_heads,
+        head_dim]``; ``out`` and the log-sum-exp stay ``[total_q, ...]``. It is the
+        result of ``run(query.index_select(0, query_rows), ...)`` without the gather. An
+        entry outside ``[0, N)`` reads row 0 and sets an error-word bit. Not combined
+        with ``append``.
         """
         _require_gpu(query, k_cache, v_cache)
         unknown = set(phases) - {"decode", "combine", "chunk"}
@@ -605,9 +614,18 @@ class VarlenAttnPlan:
             raise ValueError("Query is not on the plan's device.")
         if query.dtype not in _SUPPORTED:
             raise ValueError("varlen_attn supports bfloat16 and float16 queries.")
-        if query.ndim != 3 or query.shape[0] != self.total_q or query.shape[1] != self.n_q_heads \
+        rows_in = self.total_q if query_rows is None else query.shape[0]
+        if query.ndim != 3 or query.shape[0] != rows_in or query.shape[1] != self.n_q_heads \
                 or query.shape[2] != self.head_dim:
             raise ValueError("Query must be [total_q, n_q_heads, head_dim] as planned.")
+        if query_rows is not None:
+            if append is not None:
+                raise ValueError("query_rows and append cannot be combined.")
+            if query_rows.dtype != torch.int64 or query_rows.ndim != 1 or not query_rows.is_contiguous() \
+                    or query_rows.numel() != self.total_q or query_rows.device != self.device:
+                raise ValueError("query_rows must be contiguous int64 [total_q] on the plan's device.")
+            if query.shape[0] < 1:
+                raise ValueError("query_rows needs a query tensor of at least one row.")
         if k_cache.shape != v_cache.shape or k_cache.dtype != query.dtype or v_cache.dtype != query.dtype:
             raise ValueError("Key/value caches must match each other and the query dtype.")
         if k_cache.stride() != v_cache.stride():
@@ -634,10 +652,11 @@ class VarlenAttnPlan:
             raise ValueError("Key/value caches must be [..., n_kv_heads, head_dim] with contiguous head_dim.")
         if query.stride(2) != 1:
             query = query.contiguous()
+        out_shape = (self.total_q, self.n_q_heads, self.head_dim)
         if out is None:
-            out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
-        elif out.shape != query.shape or out.dtype != query.dtype or out.stride(2) != 1:
-            raise ValueError("out must match the query's shape and dtype.")
+            out = torch.empty(out_shape, dtype=query.dtype, device=query.device)
+        elif tuple(out.shape) != out_shape or out.dtype != query.dtype or out.stride(2) != 1:
+            raise ValueError("out must be [total_q, n_q_heads, head_dim] of the query's dtype.")
         lse = lse_out
         if lse is not None:
             if lse.dtype != torch.float32 or tuple(lse.shape) != (self.n_q_heads, self.total_q) \
@@ -668,7 +687,12 @@ class VarlenAttnPlan:
             out.data_ptr(), out.stride(0), out.stride(1),
             None if lse is None else lse.data_ptr(),
         )
-        if append is None:
+        if query_rows is not None:
+            code = _capi.lib().hx_varlen_attn_run_rows(
+                *common[:3], query_rows.data_ptr(), query.shape[0], *common[3:], *hints,
+                self.ws_ptr, self.ws_bytes, _stream_ptr(query.device))
+            _capi.check(code, "hx_varlen_attn_run_rows")
+        elif append is None:
             code = _capi.lib().hx_varlen_attn_run(
                 *common, *hints, self.ws_ptr, self.ws_bytes, _stream_ptr(query.device))
             _capi.check(code, "hx_varlen_attn_run")

@@ -55,6 +55,7 @@ extern "C" {
 #define HX_WERR_BAD_CU_SEQ 4      /* cu_seq_q not monotone or beyond total_q        */
 #define HX_WERR_GRID 8            /* more work items than the launch grid covered   */
 #define HX_WERR_PLAN_MISMATCH 16  /* run called with a shape its plan was not built for */
+#define HX_WERR_BAD_QUERY_ROW 32  /* a query row map entry outside [0, query_rows_total) */
 
 /* Human-readable text for a status code (static storage). */
 const char* hx_strerror(int code);
@@ -179,6 +180,31 @@ int hx_varlen_attn_run(const void* q, int64_t q_row_stride, int64_t q_head_strid
                        int32_t decode_items_hint, int32_t prefill_items_hint,
                        int32_t combine_seqs_hint,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * hx_varlen_attn_run with the packed query rows read through a row map: packed row t
+ * reads query row query_rows[t] of q (query_rows: device int64 [total_q]; q holds
+ * query_rows_total rows at q_row_stride). Outputs, lse and the plan stay indexed by
+ * packed row. A map entry outside [0, query_rows_total) reads row 0 and sets
+ * HX_WERR_BAD_QUERY_ROW. No reference counterpart: the shared-prefix cascade runs its
+ * prefix levels over member rows that repeat the tick's decode rows, and reads them in
+ * place instead of gathering them first.
+ */
+int hx_varlen_attn_run_rows(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                            const int64_t* query_rows, int64_t query_rows_total,
+                            const void* k_cache, const void* v_cache,
+                            int64_t kv_row_stride, int64_t kv_head_stride,
+                            int32_t num_pages, int32_t page_size,
+                            const int32_t* block_table, int32_t block_table_stride,
+                            int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                            int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                            float scale, int32_t window_left, int32_t window_right,
+                            int32_t dtype,
+                            void* out, int64_t o_row_stride, int64_t o_head_stride,
+                            float* lse,
+                            int32_t decode_items_hint, int32_t prefill_items_hint,
+                            int32_t combine_seqs_hint,
+                            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * KV append + attention in one call: the PagedBatchCache.attend sequence of the
