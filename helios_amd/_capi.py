@@ -97,6 +97,21 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i32, _i32, _i32,
          _c_void_p, _size, _c_void_p],
     ),
+    "hx_varlen_attn_run_merged": (
+        ctypes.c_int,
+        [_c_void_p, _i64, _i64,
+         _c_void_p, _c_void_p, _i64, _i64,
+         _i32, _i32, _c_void_p, _i32,
+         _i32, _i32, _i32, _i32,
+         _i32, _i32, _i32,
+         _f32, _i32, _i32, _i32,
+         _c_void_p, _i64, _i64, _c_void_p,
+         _c_void_p, _i64, _i64, _c_void_p, _i64,
+         _c_void_p, _c_void_p, _i32,
+         _c_void_p, _c_void_p, _i32,
+         _i32, _i32, _i32,
+         _c_void_p, _size, _c_void_p],
+    ),
     "hx_varlen_attn_append_run": (
         ctypes.c_int,
         [_c_void_p, _i64, _i64,

@@ -265,4 +265,54 @@ __device__ __forceinline__ float wave_sum_xor(float v, int mask_lo, int mask_hi)
 
 inline int status_from_hip(hipError_t e) { return e == hipSuccess ? HX_OK : (int)e; }
 
+// Log-sum-exp fold of attention results over disjoint key sets of one query row and head
+// h, for the 8 dims 8li..8li+7 a lane owns: parts p0..p1-1 are rows part_idx[p] (or p when
+// part_idx is null) of oa (element type T, 16-byte aligned rows) with natural-log
+// log-sum-exps lse_a[h * lse_stride + row]; rows outside [0, a_rows) are skipped. Each
+// part folds into the running (acc, m) in list order:
+//   o = fma(o_a, w_a, o * w_b) / (w_a + w_b),  m = max + log(w_a + w_b),
+// w = e^(lse - max). Up to four parts' indices, lse and rows are loaded together before
+// they are folded. Returns whether any part was folded.
+template <typename T>
+__device__ __forceinline__ bool fold_parts(float (&acc)[8], float& m, const uint16_t* oa, int64_t a_row,
+                                           int64_t a_head, const float* lse_a, int64_t lse_stride,
+                                           int64_t a_rows, int h, int li, const int32_t* part_idx,
+                                           int64_t p0, int64_t p1) {
+  bool changed = false;
+  for (int64_t pb = p0; pb < p1; pb += 4) {
+    int64_t ja[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      ja[k] = -1;
+      if (pb + k < p1) ja[k] = part_idx != nullptr ? (int64_t)part_idx[pb + k] : pb + k;
+    }
+    float la[4];
+    uint4 pv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const bool ok = ja[k] >= 0 && ja[k] < a_rows;
+      la[k] = ok ? lse_a[(int64_t)h * lse_stride + ja[k]] : -INFINITY;
+      pv[k] = ok ? *reinterpret_cast<const uint4*>(oa + ja[k] * a_row + (int64_t)h * a_head + 8 * li)
+                 : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (!(ja[k] >= 0 && ja[k] < a_rows)) continue;
+      const float mn = fmaxf(m, la[k]);
+      if (mn == -INFINITY) continue;  // neither side saw a key yet
+      const float wa = expf(la[k] - mn), wb = expf(m - mn);
+      const uint32_t w4[4] = {pv[k].x, pv[k].y, pv[k].z, pv[k].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float xa0 = Elem<T>::lo(w4[e]), xa1 = Elem<T>::hi(w4[e]);
+        acc[2 * e] = fmaf(xa0, wa, acc[2 * e] * wb) / (wa + wb);
+        acc[2 * e + 1] = fmaf(xa1, wa, acc[2 * e + 1] * wb) / (wa + wb);
+      }
+      m = mn + logf(wa + wb);
+      changed = true;
+    }
+  }
+  return changed;
+}
+
 }  // namespace hx

@@ -900,6 +900,20 @@ struct RunArgs {
   // rows when the map is given.
   const int64_t* q_rows;
   int64_t q_rows_total;
+  // Shared-prefix cascade merge done by the combine launch (mg_start == nullptr: none).
+  // Member k is the decode row of sequence mg_seq[k] (mg_of_seq[b]: sequence b's member
+  // index, or -1); it folds the level results mg_idx[mg_start[k]] .. mg_idx[mg_start[k+1]
+  // - 1] (rows of mg_o, log-sum-exps mg_lse[h * mg_lse_stride + row], mg_rows rows) into
+  // its own result by log-sum-exp.
+  const uint16_t* mg_o;
+  int64_t mg_o_row, mg_o_head;
+  const float* mg_lse;
+  int64_t mg_lse_stride, mg_rows;
+  const int32_t* mg_seq;
+  const int32_t* mg_of_seq;
+  const int32_t* mg_start;
+  const int32_t* mg_idx;
+  int32_t mg_members, mg_n_idx;
 };
 
 // Row of q that packed row r reads. A map entry outside the query tensor reads row 0 and
@@ -1410,10 +1424,100 @@ __device__ __forceinline__ void combine_store(const RunArgs& a, const CombAcc& r
     a.lse[(int64_t)qh * a.total_q + row] = r.l > 0.f ? (r.m + log2f(r.l)) * kLn2 : -INFINITY;
 }
 
+// Part range of cascade member k, clipped to the part list.
+__device__ __forceinline__ void member_parts(const RunArgs& a, int k, int64_t* p0, int64_t* p1) {
+  *p0 = max((int64_t)a.mg_start[k], (int64_t)0);
+  *p1 = min((int64_t)a.mg_start[k + 1], (int64_t)a.mg_n_idx);
+}
+
+// combine_store for the decode row of cascade member k: its result over the batch's
+// keys, rounded to T and given its log-sum-exp exactly as combine_store writes them,
+// then its levels folded in (hx::fold_parts), i.e. the bits combine_store followed by
+// hx_attn_merge's pass give. Output rows are 16-byte aligned (checked on the host).
+template <typename T>
+__device__ __forceinline__ void combine_store_member(const RunArgs& a, const CombAcc& r, int row, int qh, int ch,
+                                                     int k) {
+  const float inv = r.l > 0.f ? 1.f / r.l : 0.f;
+  uint32_t w4[4] = {hx::pack2_round<T>(r.acc[0] * inv, r.acc[1] * inv), hx::pack2_round<T>(r.acc[2] * inv, r.acc[3] * inv),
+                    hx::pack2_round<T>(r.acc[4] * inv, r.acc[5] * inv), hx::pack2_round<T>(r.acc[6] * inv, r.acc[7] * inv)};
+  float m = r.l > 0.f ? (r.m + log2f(r.l)) * kLn2 : -INFINITY;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    acc[2 * e] = hx::Elem<T>::lo(w4[e]);
+    acc[2 * e + 1] = hx::Elem<T>::hi(w4[e]);
+  }
+  int64_t p0, p1;
+  member_parts(a, k, &p0, &p1);
+  if (hx::fold_parts<T>(acc, m, a.mg_o, a.mg_o_row, a.mg_o_head, a.mg_lse, a.mg_lse_stride, a.mg_rows, qh, ch,
+                        a.mg_idx, p0, p1)) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w4[e] = hx::pack2_round<T>(acc[2 * e], acc[2 * e + 1]);
+  }
+  T* orow = reinterpret_cast<T*>(a.out) + (int64_t)row * a.o_row + (int64_t)qh * a.o_head + 8 * ch;
+  *reinterpret_cast<uint4*>(orow) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+  if (a.lse && ch == 0) a.lse[(int64_t)qh * a.total_q + row] = m;
+}
+
+// Workgroups after the combine records' in the combine launch: cascade members whose
+// decode row has one split (the decode kernel wrote its result and log-sum-exp) fold
+// their levels in place; 16 lanes per (member, head). A member whose row has more splits
+// is merged by its combine record instead.
+template <typename T, int THREADS>
+__device__ __forceinline__ void merge_unsplit_members(const RunArgs& a, int j) {
+  const Header hd = read_header(a);
+  if (!hd.ok) return;
+  const int64_t item = (int64_t)j * (THREADS / 16) + (hx::tid_x() >> 4);
+  const int li = hx::tid_x() & 15;
+  if (item >= (int64_t)a.mg_members * a.hq) return;
+  const int k = (int)(item / a.hq);
+  const int h = (int)(item - (int64_t)k * a.hq);
+  const int b = a.mg_seq[k];
+  if ((unsigned)b >= (unsigned)a.batch) return;
+  const int4 si = a.seq_info[b];
+  if (si.y != 1) return;
+  int s_first, splits;
+  decode_splits(si.z, a.win_left, &s_first, &splits);
+  if (splits > 1) return;
+  const int row = si.x;
+  if (row < 0 || row >= a.total_q) return;
+  uint16_t* po = reinterpret_cast<uint16_t*>(a.out) + (int64_t)row * a.o_row + (int64_t)h * a.o_head + 8 * li;
+  float* lb = a.lse + (int64_t)h * a.total_q + row;
+  float m = *lb;  // the row's result is normalised, with log-sum-exp m
+  const uint4 ov = *reinterpret_cast<const uint4*>(po);
+  float acc[8];
+  {
+    const uint32_t w4[4] = {ov.x, ov.y, ov.z, ov.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[2 * e] = hx::Elem<T>::lo(w4[e]);
+      acc[2 * e + 1] = hx::Elem<T>::hi(w4[e]);
+    }
+  }
+  int64_t p0, p1;
+  member_parts(a, k, &p0, &p1);
+  if (!hx::fold_parts<T>(acc, m, a.mg_o, a.mg_o_row, a.mg_o_head, a.mg_lse, a.mg_lse_stride, a.mg_rows, h, li,
+                         a.mg_idx, p0, p1))
+    return;
+  uint4 u;
+  u.x = hx::pack2_round<T>(acc[0], acc[1]);
+  u.y = hx::pack2_round<T>(acc[2], acc[3]);
+  u.z = hx::pack2_round<T>(acc[4], acc[5]);
+  u.w = hx::pack2_round<T>(acc[6], acc[7]);
+  // The 16 lanes of an entry sit in one wave: each read the old lse above, in program
+  // order before lane 0 stores the merged one.
+  *reinterpret_cast<uint4*>(po) = u;
+  if (li == 0) *lb = m;
+}
+
 template <typename T, int G, int THREADS>
 __global__ __launch_bounds__(THREADS, 4) void combine_kernel(RunArgs a) {
   constexpr int kPerRow = G * (kD / 8);  // tasks per output row
   __shared__ float sh[10][THREADS];      // (m, l, acc[8]) of every range, one column per thread
+  if (hx::wg_x() >= a.grid_comb * a.hkv) {  // the cascade merge's workgroups (mg_start set)
+    if (a.mg_start != nullptr) merge_unsplit_members<T, THREADS>(a, hx::wg_x() - a.grid_comb * a.hkv);
+    return;
+  }
   const int cs = hx::wg_x() / a.hkv;
   const int g = hx::wg_x() - cs * a.hkv;
   const Header hd = read_header(a);
@@ -1428,12 +1532,25 @@ __global__ __launch_bounds__(THREADS, 4) void combine_kernel(RunArgs a) {
   if (q0 < 0 || q0 + rows > a.total_q) return;
   const int tasks = rows * kPerRow;
   const int ranges = min(THREADS / tasks, splits);  // workgroup-uniform
+  // A decode row (its partials in the decode slots) that is a cascade member stores its
+  // merged result.
+  int member = -1;
+  if (a.mg_start != nullptr && first < a.dec_cap) {
+    const int k = a.mg_of_seq[c.x];
+    member = k < a.mg_members ? k : -1;
+  }
+  auto store = [&](const CombAcc& res, int row, int qh, int ch) {
+    if (member >= 0)
+      combine_store_member<T>(a, res, row, qh, ch, member);
+    else
+      combine_store<T>(a, res, row, qh, ch);
+  };
   if (ranges <= 1) {
     for (int t = hx::tid_x(); t < tasks; t += THREADS) {
       const int r = t / kPerRow;
       const int h = (t - r * kPerRow) >> 4, ch = t & 15;
       const CombAcc res = combine_range<T>(a, (int64_t)first + (int64_t)r * splits, g * G + h, ch, 0, splits);
-      combine_store<T>(a, res, q0 + r, g * G + h, ch);
+      store(res, q0 + r, g * G + h, ch);
     }
     return;
   }
@@ -1470,7 +1587,7 @@ __global__ __launch_bounds__(THREADS, 4) void combine_kernel(RunArgs a) {
         for (int e = 0; e < 8; ++e) res.acc[e] += wq * sh[2 + e][col];
       }
     }
-    combine_store<T>(a, res, q0 + r, g * G + h, ch);
+    store(res, q0 + r, g * G + h, ch);
   }
 }
 
@@ -2045,11 +2162,16 @@ int launch_run(const RunArgs& a, hipStream_t s) {
                        0, s, a);
   if (a.grid_pf > 0)
     hipLaunchKernelGGL((chunk_kernel<T, G>), dim3((unsigned)(a.grid_pf * a.hkv)), dim3(kChunkThreads), 0, s, a);
-  if (a.grid_comb > 0) {
-    if (ceil_div(a.max_k, kSplit) > kCombSmallSplits)
-      hipLaunchKernelGGL((combine_kernel<T, G, 512>), dim3((unsigned)(a.grid_comb * a.hkv)), dim3(512), 0, s, a);
+  // A cascade merge adds workgroups for its members whose rows have no combine record;
+  // it runs in this launch whenever it is given (the call that holds the combine phase).
+  const bool wide = ceil_div(a.max_k, kSplit) > kCombSmallSplits;
+  const int64_t merge_wgs = a.mg_start != nullptr ? ceil_div((int64_t)a.mg_members * a.hq, (wide ? 512 : 256) / 16) : 0;
+  if (a.grid_comb > 0 || merge_wgs > 0) {
+    const unsigned grid = (unsigned)((int64_t)a.grid_comb * a.hkv + merge_wgs);
+    if (wide)
+      hipLaunchKernelGGL((combine_kernel<T, G, 512>), dim3(grid), dim3(512), 0, s, a);
     else
-      hipLaunchKernelGGL((combine_kernel<T, G, 256>), dim3((unsigned)(a.grid_comb * a.hkv)), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((combine_kernel<T, G, 256>), dim3(grid), dim3(256), 0, s, a);
   }
   return hx::status_from_hip(hipGetLastError());
 }
@@ -2223,6 +2345,19 @@ int hx_varlen_attn_plan(const int32_t* cu_seq_q, const int32_t* cu_seq_k,
 
 namespace {
 
+struct MergeSpec {
+  const void* level_out;
+  int64_t level_row, level_head;
+  const float* level_lse;
+  int64_t level_rows;
+  const int32_t* member_seq;
+  const int32_t* member_of_seq;
+  int32_t n_members;
+  const int32_t* part_start;
+  const int32_t* part_idx;
+  int32_t n_parts;
+};
+
 struct AppendSpec {
   const void* k_new;
   const void* v_new;
@@ -2245,7 +2380,8 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
              float* lse,
              int32_t decode_items_hint, int32_t prefill_items_hint,
              int32_t combine_seqs_hint,
-             void* workspace, size_t workspace_bytes, void* stream, const AppendSpec* app) {
+             void* workspace, size_t workspace_bytes, void* stream, const AppendSpec* app,
+             const MergeSpec* mg = nullptr) {
   int st = check_shape(batch, max_q, max_k, n_q_heads, n_kv_heads, head_dim);
   if (st != HX_OK) return st;
   if (dtype != HX_DTYPE_BF16 && dtype != HX_DTYPE_FP16) return HX_E_UNSUPPORTED;
@@ -2320,6 +2456,37 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
   a.app_wgs = 0;
   a.q_rows = q_rows;
   a.q_rows_total = q_rows_total;
+  a.mg_o = nullptr;
+  a.mg_o_row = a.mg_o_head = 0;
+  a.mg_lse = nullptr;
+  a.mg_lse_stride = a.mg_rows = 0;
+  a.mg_seq = a.mg_of_seq = a.mg_start = a.mg_idx = nullptr;
+  a.mg_members = a.mg_n_idx = 0;
+  if (mg != nullptr && mg->n_members > 0) {
+    // Tuned shapes only (the merge runs in the combine launch); 16-byte rows for the
+    // merged stores and loads; the lse of every row (the unsplit members' merge reads it).
+    if (!tuned_shape(n_q_heads / n_kv_heads, head_dim)) return HX_E_UNSUPPORTED;
+    if (!lse || !mg->level_out || !mg->level_lse || !mg->member_seq || !mg->member_of_seq ||
+        !mg->part_start || (mg->n_parts > 0 && !mg->part_idx))
+      return HX_E_INVALID_ARG;
+    if (mg->level_rows < 0 || mg->n_parts < 0 || mg->level_row < 0 || mg->level_head < 0)
+      return HX_E_INVALID_ARG;
+    if ((uintptr_t)out % 16 || o_row_stride % 8 || o_head_stride % 8 || (uintptr_t)mg->level_out % 16 ||
+        mg->level_row % 8 || mg->level_head % 8)
+      return HX_E_INVALID_ARG;
+    a.mg_o = static_cast<const uint16_t*>(mg->level_out);
+    a.mg_o_row = mg->level_row;
+    a.mg_o_head = mg->level_head;
+    a.mg_lse = mg->level_lse;
+    a.mg_lse_stride = mg->level_rows;
+    a.mg_rows = mg->level_rows;
+    a.mg_seq = mg->member_seq;
+    a.mg_of_seq = mg->member_of_seq;
+    a.mg_start = mg->part_start;
+    a.mg_idx = mg->part_idx;
+    a.mg_members = mg->n_members;
+    a.mg_n_idx = mg->n_parts;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int G = n_q_heads / n_kv_heads;
   const bool tuned = tuned_shape(G, head_dim);
@@ -2423,6 +2590,44 @@ int hx_varlen_attn_run_rows(const void* q, int64_t q_row_stride, int64_t q_head_
                   scale, window_left, window_right, dtype, out, o_row_stride, o_head_stride, lse,
                   decode_items_hint, prefill_items_hint, combine_seqs_hint, workspace,
                   workspace_bytes, stream, nullptr);
+}
+
+int hx_varlen_attn_run_merged(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                              const void* k_cache, const void* v_cache,
+                              int64_t kv_row_stride, int64_t kv_head_stride,
+                              int32_t num_pages, int32_t page_size,
+                              const int32_t* block_table, int32_t block_table_stride,
+                              int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                              int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                              float scale, int32_t window_left, int32_t window_right,
+                              int32_t dtype,
+                              void* out, int64_t o_row_stride, int64_t o_head_stride,
+                              float* lse,
+                              const void* level_out, int64_t level_row_stride, int64_t level_head_stride,
+                              const float* level_lse, int64_t level_rows,
+                              const int32_t* member_seq, const int32_t* member_of_seq, int32_t n_members,
+                              const int32_t* part_start, const int32_t* part_idx, int32_t n_parts,
+                              int32_t decode_items_hint, int32_t prefill_items_hint,
+                              int32_t combine_seqs_hint,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  if (n_members < 0) return HX_E_INVALID_ARG;
+  MergeSpec mg;
+  mg.level_out = level_out;
+  mg.level_row = level_row_stride;
+  mg.level_head = level_head_stride;
+  mg.level_lse = level_lse;
+  mg.level_rows = level_rows;
+  mg.member_seq = member_seq;
+  mg.member_of_seq = member_of_seq;
+  mg.n_members = n_members;
+  mg.part_start = part_start;
+  mg.part_idx = part_idx;
+  mg.n_parts = n_parts;
+  return run_impl(q, q_row_stride, q_head_stride, nullptr, 0, k_cache, v_cache, kv_row_stride,
+                  kv_head_stride, num_pages, page_size, block_table, block_table_stride, batch,
+                  total_q, max_q, max_k, n_q_heads, n_kv_heads, head_dim, scale, window_left,
+                  window_right, dtype, out, o_row_stride, o_head_stride, lse, decode_items_hint,
+                  prefill_items_hint, combine_seqs_hint, workspace, workspace_bytes, stream, nullptr, &mg);
 }
 
 int hx_varlen_attn_append_run(const void* q, int64_t q_row_stride, int64_t q_head_stride,

@@ -253,40 +253,9 @@ __global__ __launch_bounds__(256) void merge_vec_kernel(uint16_t* out, int64_t o
       acc[2 * e + 1] = hx::Elem<T>::hi(w4[e]);
     }
   }
-  bool changed = false;
-  for (int64_t pb = p0; pb < p1; pb += 4) {
-    int64_t ja[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      ja[k] = -1;
-      if (pb + k < p1) ja[k] = part_start != nullptr ? (int64_t)part_idx[pb + k] : pb + k;
-    }
-    float la[4];
-    uint4 pv[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const bool ok = ja[k] >= 0 && ja[k] < total_a;
-      la[k] = ok ? lse_a[(int64_t)h * total_a + ja[k]] : -INFINITY;
-      pv[k] = ok ? *reinterpret_cast<const uint4*>(oa + ja[k] * a_row + (int64_t)h * a_head + 8 * li)
-                 : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      if (!(ja[k] >= 0 && ja[k] < total_a)) continue;
-      const float mn = fmaxf(m, la[k]);
-      if (mn == -INFINITY) continue;  // neither side saw a key yet
-      const float wa = expf(la[k] - mn), wb = expf(m - mn);
-      const uint32_t w4[4] = {pv[k].x, pv[k].y, pv[k].z, pv[k].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float xa0 = hx::Elem<T>::lo(w4[e]), xa1 = hx::Elem<T>::hi(w4[e]);
-        acc[2 * e] = fmaf(xa0, wa, acc[2 * e] * wb) / (wa + wb);
-        acc[2 * e + 1] = fmaf(xa1, wa, acc[2 * e + 1] * wb) / (wa + wb);
-      }
-      m = mn + logf(wa + wb);
-      changed = true;
-    }
-  }
+  // Parts outside [0, total_a) are skipped (o_a holds total_a rows).
+  const bool changed = hx::fold_parts<T>(acc, m, oa, a_row, a_head, lse_a, total_a, total_a, h, li,
+                                         part_start != nullptr ? part_idx : nullptr, p0, p1);
   if (!changed) return;
   uint4 u;
   u.x = hx::pack2_round<T>(acc[0], acc[1]);

@@ -52,6 +52,21 @@ def describe_error_word(word: int) -> str:
     return "; ".join(parts) if parts else "no error"
 
 
+class MergeParts(NamedTuple):
+    """A shared-prefix cascade merge for ``VarlenAttnPlan.run(..., merge=...)``: member k
+    is the decode row of sequence ``member_seq[k]`` (``member_of_seq[b]``: sequence b's
+    member index or -1); its parts are rows ``part_idx[part_start[k]:part_start[k + 1]]``
+    of ``level_out`` ``[A, H, 128]`` with log-sum-exps ``level_lse`` ``[H, A]``. All on the
+    device; the int arrays are contiguous int32."""
+
+    level_out: torch.Tensor
+    level_lse: torch.Tensor
+    member_seq: torch.Tensor
+    member_of_seq: torch.Tensor
+    part_start: torch.Tensor
+    part_idx: torch.Tensor
+
+
 class AuxRequest(NamedTuple):
     """Auxiliary outputs of varlen_attn (same field as torch's AuxRequest)."""
 
@@ -209,8 +224,9 @@ def attn_merge(out: torch.Tensor, lse_out: torch.Tensor, o_a: torch.Tensor, lse_
     lse_out[:, rows[j]])``. With ``parts = (part_start, part_idx)`` (int32 ``[n + 1]`` and
     ``[P]``), entry j merges the o_a rows ``part_idx[part_start[j]:part_start[j + 1]]``
     into ``out[rows[j]]`` in one pass. ``out`` ``[T, H, 128]`` and ``o_a`` ``[A, H, 128]``
-    (contiguous last dim), ``lse_out`` fp32 ``[H, T]``, ``lse_a`` fp32 ``[H, A]`` (or a
-    column slice of a wider array), ``rows`` int64 ``[n]`` without repeats."""
+    (contiguous last dim), ``lse_out`` fp32 ``[H, T]``, ``lse_a`` fp32 ``[H, A]``
+    contiguous, ``rows`` int64 ``[n]`` without repeats. A part index outside ``[0, A)``
+    is skipped."""
     device = _require_gpu(out, lse_out, o_a, lse_a, rows)
     if out.ndim != 3 or o_a.ndim != 3 or out.shape[1:] != o_a.shape[1:] or out.dtype != o_a.dtype:
         raise ValueError("out and o_a must be [rows, heads, head_dim] of one dtype.")
@@ -220,10 +236,10 @@ def attn_merge(out: torch.Tensor, lse_out: torch.Tensor, o_a: torch.Tensor, lse_
     n = rows.numel()
     if lse_out.dtype != torch.float32 or tuple(lse_out.shape) != (heads, out.shape[0]) or not lse_out.is_contiguous():
         raise ValueError("lse_out must be contiguous float32 [heads, rows].")
-    # lse_a may be a column slice of a wider [heads, total] array (rows stride(0) apart).
-    if lse_a.dtype != torch.float32 or tuple(lse_a.shape) != (heads, n_a) or (n_a > 0 and lse_a.stride(1) != 1) \
-            or (heads > 1 and lse_a.stride(0) < n_a):
-        raise ValueError("lse_a must be float32 [heads, rows] with contiguous rows.")
+    # The kernel bounds part indices by lse_a's row stride, so that stride must be o_a's
+    # row count: lse_a contiguous [heads, n_a].
+    if lse_a.dtype != torch.float32 or tuple(lse_a.shape) != (heads, n_a) or not lse_a.is_contiguous():
+        raise ValueError("lse_a must be contiguous float32 [heads, rows].")
     if rows.dtype != torch.int64 or rows.ndim != 1 or not rows.is_contiguous():
         raise ValueError("rows must be contiguous int64 [n].")
     start_ptr = idx_ptr = None
@@ -245,7 +261,7 @@ def attn_merge(out: torch.Tensor, lse_out: torch.Tensor, o_a: torch.Tensor, lse_
         raise ValueError("attention outputs must be bfloat16 or float16.")
     code = _capi.lib().hx_attn_merge(
         out.data_ptr(), out.stride(0), out.stride(1), lse_out.data_ptr(), out.shape[0],
-        o_a.data_ptr(), o_a.stride(0), o_a.stride(1), lse_a.data_ptr(), lse_a.stride(0) if heads > 1 else n_a,
+        o_a.data_ptr(), o_a.stride(0), o_a.stride(1), lse_a.data_ptr(), n_a,
         rows.data_ptr(), start_ptr, idx_ptr, n_parts, n, heads, o_a.shape[2], dtype, _stream_ptr(device),
     )
     _capi.check(code, "hx_attn_merge")
@@ -587,6 +603,7 @@ class VarlenAttnPlan:
         phases: tuple[str, ...] = ("decode", "chunk", "combine"),
         append: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
         query_rows: torch.Tensor | None = None,
+        merge: MergeParts | None = None,
     ) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
         """Attention for one layer. ``phases`` launches a subset of the three kernels
         (decode splits, chunk rows, split combine); a full result needs all three, with
@@ -605,6 +622,11 @@ class VarlenAttnPlan:
         result of ``run(query.index_select(0, query_rows), ...)`` without the gather. An
         entry outside ``[0, N)`` reads row 0 and sets an error-word bit. Not combined
         with ``append``.
+
+        ``merge`` (``MergeParts``) folds a shared-prefix cascade's level results into its
+        members' rows inside the combine launch: the bits of this run followed by
+        ``attn_merge`` over the same parts, one launch fewer. It needs the combine phase
+        and the log-sum-exp output (``return_lse`` or ``lse_out``), on the tuned shapes.
         """
         _require_gpu(query, k_cache, v_cache)
         unknown = set(phases) - {"decode", "combine", "chunk"}
@@ -687,7 +709,32 @@ class VarlenAttnPlan:
             out.data_ptr(), out.stride(0), out.stride(1),
             None if lse is None else lse.data_ptr(),
         )
-        if query_rows is not None:
+        if merge is not None:
+            if append is not None or query_rows is not None:
+                raise ValueError("merge cannot be combined with append or query_rows.")
+            if "combine" not in phases or lse is None or not self.tuned:
+                raise ValueError("merge needs the combine phase, the lse output and a tuned shape.")
+            lo, ll = merge.level_out, merge.level_lse
+            n_a = lo.shape[0] if lo.ndim == 3 else -1
+            if lo.ndim != 3 or lo.shape[1:] != (self.n_q_heads, self.head_dim) or lo.dtype != query.dtype \
+                    or lo.stride(2) != 1 or lo.device != self.device:
+                raise ValueError("merge.level_out must be [rows, n_q_heads, head_dim] of the query's dtype.")
+            if ll.dtype != torch.float32 or tuple(ll.shape) != (self.n_q_heads, n_a) or not ll.is_contiguous():
+                raise ValueError("merge.level_lse must be contiguous float32 [n_q_heads, rows].")
+            for name in ("member_seq", "member_of_seq", "part_start", "part_idx"):
+                t = getattr(merge, name)
+                if t.dtype != torch.int32 or t.ndim != 1 or not t.is_contiguous() or t.device != self.device:
+                    raise ValueError(f"merge.{name} must be a contiguous int32 vector on the device.")
+            n_members = merge.member_seq.numel()
+            if merge.part_start.numel() != n_members + 1 or merge.member_of_seq.numel() != self.batch:
+                raise ValueError("merge.part_start needs members + 1 entries and member_of_seq one per sequence.")
+            code = _capi.lib().hx_varlen_attn_run_merged(
+                *common, lo.data_ptr(), lo.stride(0), lo.stride(1), ll.data_ptr(), n_a,
+                merge.member_seq.data_ptr(), merge.member_of_seq.data_ptr(), n_members,
+                merge.part_start.data_ptr(), merge.part_idx.data_ptr(), merge.part_idx.numel(),
+                *hints, self.ws_ptr, self.ws_bytes, _stream_ptr(query.device))
+            _capi.check(code, "hx_varlen_attn_run_merged")
+        elif query_rows is not None:
             code = _capi.lib().hx_varlen_attn_run_rows(
                 *common[:3], query_rows.data_ptr(), query.shape[0], *common[3:], *hints,
                 self.ws_ptr, self.ws_bytes, _stream_ptr(query.device))

@@ -207,6 +207,39 @@ int hx_varlen_attn_run_rows(const void* q, int64_t q_row_stride, int64_t q_head_
                             void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * hx_varlen_attn_run whose combine launch also does a shared-prefix cascade merge (the
+ * work of hx_attn_merge after the run, without its launch). Member k is the decode row of
+ * sequence member_seq[k] (member_of_seq[b]: sequence b's member index or -1, [batch]);
+ * its parts are rows part_idx[part_start[k]] .. part_idx[part_start[k + 1] - 1] of
+ * level_out ([level_rows, n_q_heads, 128], strides in elements) with natural-log
+ * log-sum-exps level_lse[h * level_rows + row] (contiguous [n_q_heads, level_rows]). The
+ * members' rows of out and lse get exactly what hx_varlen_attn_run followed by
+ * hx_attn_merge over the same parts gives, bit for bit. Call it with the combine phase
+ * (combine_seqs_hint != 0 or -1): the merge runs in this call's combine launch, which is
+ * launched whenever n_members > 0. lse must be given; out and level_out need 16-byte
+ * aligned rows (strides multiples of 8 elements); head_dim 128 with n_q_heads /
+ * n_kv_heads in {1, 2, 4, 8} (HX_E_UNSUPPORTED otherwise). No reference counterpart.
+ */
+int hx_varlen_attn_run_merged(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                              const void* k_cache, const void* v_cache,
+                              int64_t kv_row_stride, int64_t kv_head_stride,
+                              int32_t num_pages, int32_t page_size,
+                              const int32_t* block_table, int32_t block_table_stride,
+                              int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                              int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                              float scale, int32_t window_left, int32_t window_right,
+                              int32_t dtype,
+                              void* out, int64_t o_row_stride, int64_t o_head_stride,
+                              float* lse,
+                              const void* level_out, int64_t level_row_stride, int64_t level_head_stride,
+                              const float* level_lse, int64_t level_rows,
+                              const int32_t* member_seq, const int32_t* member_of_seq, int32_t n_members,
+                              const int32_t* part_start, const int32_t* part_idx, int32_t n_parts,
+                              int32_t decode_items_hint, int32_t prefill_items_hint,
+                              int32_t combine_seqs_hint,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * KV append + attention in one call: the PagedBatchCache.attend sequence of the
  * reference (paged_cache.py:301-332 and :501-520: _write, i.e. index_copy_ of the new
  * rows into k_cache / v_cache at write_slots, then varlen_attn on the updated pool).
@@ -361,9 +394,9 @@ int hx_qk_norm_rope_append(const void* q, int64_t q_row_stride, int64_t q_head_s
  *   lse = m + log(e^(lse_a - m) + e^(lse_b - m))
  * in fp32, rounded to the element type once at the end. lse arrays are fp32
  * [n_heads, total] (the layout of hx_varlen_attn's lse): head h of row j is
- * lse_a[h * total_a + j], so lse_a may point into a wider array. rows must not repeat
- * within one call; a part index outside [0, total_a) is skipped. Rows where every lse
- * is -inf are left unchanged. head_dim must be 128.
+ * lse_a[h * total_a + j], and o_a holds total_a rows. rows must not repeat within one
+ * call; a part index outside [0, total_a) is skipped. Rows where every lse is -inf are
+ * left unchanged. head_dim must be 128.
  */
 int hx_attn_merge(void* out, int64_t out_row_stride, int64_t out_head_stride,
                   float* lse_out, int64_t total_out,

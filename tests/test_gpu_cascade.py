@@ -311,3 +311,48 @@ def test_overlapped_streams_give_the_same_bits(device, cascade, always_cascade):
             _compare(outs[-1][0].transpose(0, 1).float().cpu().numpy(), want, "overlap")
         batch.advance_packed()
     assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])
+
+
+def test_merge_in_the_combine_launch_equals_the_merge_pass(device, always_cascade):
+    """``run(..., merge=...)`` folds the levels into the members' rows in batch B's combine
+    launch. Its out and lse equal batch B's run followed by ``attn_merge`` over the same
+    parts, bit for bit, for members whose rows have one split after their levels (merged
+    by the launch's extra workgroups) and members with several (merged by their combine
+    records), and it leaves other rows as the run writes them."""
+    say("cascade merge folded into the combine launch")
+    pool = _pool(device, pages=200)
+    cached = [8 * 256 + 5, 8 * 256 + 40, 8 * 256 + 300, 5000, 6100, 3 * 256 + 10, 7000, 2100, 600, 300]
+    _prefix, caches = _shared_caches(pool, cached, prefix_pages=8)
+    batch = PagedBatchCache(caches)
+    batch.prepare(1)
+    cas = batch._cascade
+    assert cas is not None
+    levels = _PrefixCascade.levels(batch, [1] * len(caches))
+    shift = [0] * len(caches)
+    for _ref, _first, end, members in levels:
+        for b in members:
+            shift[b] = max(shift[b], end)
+    splits = {b: (cached[b] + 1 - 256 * shift[b] - 1) // 256 + 1 for b in range(len(caches)) if shift[b]}
+    assert 1 in splits.values() and max(splits.values()) > 1, splits
+    g = torch.Generator(device="cpu").manual_seed(9)
+    q = torch.randn((len(caches), 32, 128), generator=g).to(torch.bfloat16).to(device)
+    kp, vp = pool.keys[0], pool.values[0]
+    rows_a, (out_rows, part_start, part_idx) = cas.rows_a, cas.merge
+    o_a, lse_a = cas.plan_a.run(q, kp, vp, cas.bt_a, return_lse=True, query_rows=rows_a)
+    want, want_lse = cas.plan_b.run(q, kp, vp, cas.bt_b, return_lse=True)
+    plain = want.clone()
+    ops.attn_merge(want, want_lse, o_a, lse_a, out_rows, parts=(part_start, part_idx))
+    member_seq, member_of_seq = cas.members
+    merge = ops.MergeParts(o_a, lse_a, member_seq, member_of_seq, part_start, part_idx)
+    got, got_lse = cas.plan_b.run(q, kp, vp, cas.bt_b, return_lse=True, merge=merge)
+    torch.cuda.synchronize()
+    assert cas.plan_b.error_word() == 0
+    assert torch.equal(got, want)
+    assert torch.equal(got_lse, want_lse)
+    members = set(out_rows.tolist())
+    assert not torch.equal(got, plain)  # the levels changed the members' rows
+    for r in range(len(caches)):
+        if r not in members:
+            assert torch.equal(got[r], plain[r])
+    with pytest.raises(ValueError, match="combine phase"):
+        cas.plan_b.run(q, kp, vp, cas.bt_b, return_lse=True, merge=merge, phases=("decode",))
