@@ -25,12 +25,15 @@
 //   chunk_kernel    prefill chunks: 8 waves per workgroup (2 per SIMD), each wave owning
 //                   32 query rows of one head; 64-key K / V tiles are copied from HBM
 //                   straight into LDS (the next tile's copies in flight while the current
-//                   one is consumed; V read back transposed); S^T = K Q^T and O^T = V^T P^T both
-//                   run on 16x16x32 MFMA with online softmax in between. When the chunk
+//                   one is consumed; V read back transposed); S^T = K Q^T and O^T = V^T P^T
+//                   both run on 16x16x32 MFMA with online softmax in between. When the chunk
 //                   rows alone would not fill the GPU, row blocks are split over their key
 //                   tiles and write partials like decode splits.
 //   combine_kernel  merges the partials of each long decode row and each split chunk row
 //                   in split order, so results do not depend on scheduling. Runs last.
+//                   Given a shared-prefix cascade merge, it also folds the cascade's level
+//                   results into the member rows: in the member's combine record, or, for
+//                   a member whose row has one split, in workgroups after the records.
 
 #include "hx_common.h"
 
