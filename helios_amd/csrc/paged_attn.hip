@@ -1599,6 +1599,9 @@ constexpr int kChunkThreads = 512;     // 8 waves: 2 per SIMD
 constexpr float kLazyLog2 = 8.f;       // softmax terms stay <= 2^8 between max updates
 constexpr int kTileRowBytes = kD * 2;  // one key row of one KV head in a tile: 256 B
 constexpr int kTileBytes = kTile * kTileRowBytes;  // 16 KiB
+// Instruction classes of __builtin_amdgcn_sched_group_barrier's mask.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
 // Tile layout in LDS. Two K and two V tiles of 64 key rows x 256 B, each its own LDS
 // variable (64 KiB in all). The tiles arrive by direct-to-LDS buffer loads: one wave
 // instruction writes 1 KiB, four whole key rows, so rows cannot be padded; the 16-byte
@@ -1810,6 +1813,21 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
     // V operands of the first P V key step, in flight during the softmax.
     uint4 vf0[8];
     read_v(vl, 0, vf0);
+    // Issue order for this block: 8 K fragment reads, then one more read after each pair
+    // of QK MFMAs (a K read 8 fragments ahead of its use), then the V reads two per MFMA
+    // pair under the last 16 MFMAs. Left to itself, hipcc issues each K read one or two
+    // MFMA pairs ahead and waits for it at lgkmcnt(0).
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+    }
 
     // Mask only where the tile is not fully visible to every row of this wave (a
     // wave-uniform test, evaluated on the scalar unit).
@@ -1907,6 +1925,15 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
         oacc[db][rb] = E::mfma16x16x32(hx::as_v8<T>(vf1[db]), pb[1][rb], oacc[db][rb]);
+    // The second key step's 16 V reads go out two per MFMA under the first step's
+    // first 8 MFMAs (hipcc otherwise issues them four at a time between the second
+    // step's MFMAs, each pair waiting for its reads).
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 24, 1);
   };
 
   if (t_begin < t_end) load_tile(t_begin, k_lds0, v_lds0);
