@@ -13,7 +13,7 @@ HEADER_PATH = Path(__file__).resolve().parent.parent / "include" / "helios_paged
 
 HX_OK = 0
 # hx_abi_version() of the library these signatures describe (bumped on any signature change).
-ABI_VERSION = 4
+ABI_VERSION = 5
 HX_E_INVALID_ARG = -1
 HX_E_UNSUPPORTED = -2
 HX_E_WORKSPACE = -3
@@ -107,6 +107,23 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _f32, _i32, _i32, _i32,
          _c_void_p, _i64, _i64, _c_void_p,
          _c_void_p, _i64, _i64, _c_void_p, _i64,
+         _c_void_p, _c_void_p, _i32,
+         _c_void_p, _c_void_p, _i32,
+         _i32, _i32, _i32,
+         _c_void_p, _size, _c_void_p],
+    ),
+    "hx_varlen_attn_run_cascade": (
+        ctypes.c_int,
+        [_c_void_p, _i64, _i64,
+         _c_void_p, _c_void_p, _i64, _i64,
+         _i32, _i32, _c_void_p, _i32,
+         _i32, _i32, _i32, _i32,
+         _i32, _i32, _i32,
+         _f32, _i32, _i32, _i32,
+         _c_void_p, _i64, _i64, _c_void_p,
+         _c_void_p, _i64, _i64, _c_void_p, _i64,
+         _i32, _i32, _i32,
+         _i32, _c_void_p, _size,
          _c_void_p, _c_void_p, _i32,
          _c_void_p, _c_void_p, _i32,
          _i32, _i32, _i32,

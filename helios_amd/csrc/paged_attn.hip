@@ -917,7 +917,46 @@ struct RunArgs {
   const int32_t* mg_start;
   const int32_t* mg_idx;
   int32_t mg_members, mg_n_idx;
+  // Combine records of a second plan (a cascade's level batch, whose decode and chunk
+  // phases ran before this launch) done by sc_wgs workgroups after the decode launch's
+  // own (sc_wgs == 0: none): that plan's header, lists, partials, outputs and shape,
+  // i.e. the fields a combine launch of that plan reads (side_combine_args).
+  int32_t* sc_hdr;
+  const int4* sc_comb_seqs;
+  float2* sc_part_ml;
+  uint16_t* sc_part_o;
+  uint8_t* sc_out;
+  float* sc_lse;
+  int64_t sc_o_row, sc_o_head;
+  int64_t sc_dec_cap, sc_slot_cap;
+  int32_t sc_batch, sc_max_q, sc_max_k, sc_total_q, sc_grid_comb;
+  int32_t sc_wgs;
 };
+
+// The arguments of the second plan's combine launch (RunArgs::sc_*): the same pools,
+// heads and scale, that plan's workspace and outputs, no cascade merge of its own.
+__host__ __device__ inline RunArgs side_combine_args(const RunArgs& a) {
+  RunArgs b = a;
+  b.hdr = a.sc_hdr;
+  b.comb_seqs = a.sc_comb_seqs;
+  b.part_ml = a.sc_part_ml;
+  b.part_o = a.sc_part_o;
+  b.out = a.sc_out;
+  b.lse = a.sc_lse;
+  b.o_row = a.sc_o_row;
+  b.o_head = a.sc_o_head;
+  b.dec_cap = a.sc_dec_cap;
+  b.slot_cap = a.sc_slot_cap;
+  b.batch = a.sc_batch;
+  b.max_q = a.sc_max_q;
+  b.max_k = a.sc_max_k;
+  b.total_q = a.sc_total_q;
+  b.grid_comb = a.sc_grid_comb;
+  b.mg_start = nullptr;
+  b.mg_members = 0;
+  b.sc_wgs = 0;
+  return b;
+}
 
 // Row of q that packed row r reads. A map entry outside the query tensor reads row 0 and
 // is reported in the error word.
@@ -1063,14 +1102,21 @@ __device__ __forceinline__ void rows_reduce_scatter(const float (&x)[NV], float 
   }
 }
 
-// APPEND_ROWS: the launch also holds the append workgroups (a.app_wgs after the decode
-// workgroups); a separate instantiation, so decode-only launches carry no trace of them.
+template <typename T, int G, int THREADS>
+__device__ __forceinline__ void combine_records(const RunArgs& a, int wg, float (&sh)[10][THREADS]);
+
+// EXTRA: workgroups of the launch after the decode workgroups. kExtraAppend: a.app_wgs
+// append workgroups. kExtraCombine: those, then a.sc_wgs workgroups running the combine
+// records of a second plan (a cascade's level batch). Each kind is its own
+// instantiation, so launches without them carry no trace of them (with the combine code
+// inlined, hipcc allocates the decode path for four waves per SIMD instead of three).
 // Occupancy: three workgroups per CU (at most 168 VGPRs) up to G = 4.
+constexpr int kExtraNone = 0, kExtraAppend = 1, kExtraCombine = 2;
 template <typename T, int G>
 constexpr int decode_min_wgs() {
   return G <= 4 ? 3 : 2;
 }
-template <typename T, int G, bool APPEND_ROWS>
+template <typename T, int G, int EXTRA>
 __global__ __launch_bounds__(kThreads, (decode_min_wgs<T, G>())) void decode_kernel(RunArgs a) {
   typedef hx::Elem<T> E;
   constexpr int NV = G * 8;  // o values per lane: G heads x 8 dims
@@ -1085,10 +1131,16 @@ __global__ __launch_bounds__(kThreads, (decode_min_wgs<T, G>())) void decode_ker
   // workgroups an XCD receives are the KV heads of one split; each XCD then streams whole
   // token rows of the pages it reads (about 4 % faster than one head per XCD). The grid
   // covers the work items rounded up to a multiple of kXcds.
-  if constexpr (APPEND_ROWS) {
+  if constexpr (EXTRA != kExtraNone) {
     const int dec_wgs = (a.grid_dec + kXcds - 1) / kXcds * kXcds * a.hkv;
-    if (hx::wg_x() >= dec_wgs) {  // append workgroups follow the decode workgroups
-      append_rows<T>(a, hx::wg_x() - dec_wgs, a.app_wgs);
+    if (hx::wg_x() >= dec_wgs) {  // append, then combine workgroups follow the decode ones
+      const int j = hx::wg_x() - dec_wgs;
+      if (j < a.app_wgs) {
+        append_rows<T>(a, j, a.app_wgs);
+      } else if constexpr (EXTRA == kExtraCombine) {
+        __shared__ float comb_sh[10][kThreads];
+        combine_records<T, G, kThreads>(side_combine_args(a), j - a.app_wgs, comb_sh);
+      }
       return;
     }
   }
@@ -1513,21 +1565,23 @@ __device__ __forceinline__ void merge_unsplit_members(const RunArgs& a, int j) {
   if (li == 0) *lb = m;
 }
 
+// Combine record cs = wg / hkv of KV head wg % hkv: workgroup wg of a combine launch, or
+// of the extra combine workgroups of a decode launch (then with the other plan's
+// arguments, side_combine_args). sh: (m, l, acc[8]) of every range, one column per thread.
 template <typename T, int G, int THREADS>
-__global__ __launch_bounds__(THREADS, 4) void combine_kernel(RunArgs a) {
+__device__ __forceinline__ void combine_records(const RunArgs& a, int wg, float (&sh)[10][THREADS]) {
   constexpr int kPerRow = G * (kD / 8);  // tasks per output row
-  __shared__ float sh[10][THREADS];      // (m, l, acc[8]) of every range, one column per thread
-  if (hx::wg_x() >= a.grid_comb * a.hkv) {  // the cascade merge's workgroups (mg_start set)
-    if (a.mg_start != nullptr) merge_unsplit_members<T, THREADS>(a, hx::wg_x() - a.grid_comb * a.hkv);
-    return;
-  }
-  const int cs = hx::wg_x() / a.hkv;
-  const int g = hx::wg_x() - cs * a.hkv;
+  const int cs = wg / a.hkv;
+  const int g = wg - cs * a.hkv;
   const Header hd = read_header(a);
   const int4 c = a.comb_seqs[cs];  // cs < grid_comb <= max_comb
-  if (!hd.ok) return;
+  if (!hd.ok) {
+    // read_header reports for the launch's first workgroup; extra workgroups report here.
+    if (wg == 0 && hx::wg_x() != 0 && hx::tid_x() == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_PLAN_MISMATCH);
+    return;
+  }
   const int n_comb = hd.counts.z;
-  if (hx::wg_x() == 0 && hx::tid_x() == 0 && n_comb > a.grid_comb) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
+  if (wg == 0 && hx::tid_x() == 0 && n_comb > a.grid_comb) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
   if (cs >= n_comb) return;
   const int first = c.y, splits = c.z & 0xffffff, rows = (c.z >> 24) + 1, q0 = c.w;
   if ((unsigned)c.x >= (unsigned)a.batch || first < 0 || splits < 1 || rows > kCombRows) return;
@@ -1592,6 +1646,16 @@ __global__ __launch_bounds__(THREADS, 4) void combine_kernel(RunArgs a) {
     }
     store(res, q0 + r, g * G + h, ch);
   }
+}
+
+template <typename T, int G, int THREADS>
+__global__ __launch_bounds__(THREADS, 4) void combine_kernel(RunArgs a) {
+  __shared__ float sh[10][THREADS];
+  if (hx::wg_x() >= a.grid_comb * a.hkv) {  // the cascade merge's workgroups (mg_start set)
+    if (a.mg_start != nullptr) merge_unsplit_members<T, THREADS>(a, hx::wg_x() - a.grid_comb * a.hkv);
+    return;
+  }
+  combine_records<T, G, THREADS>(a, hx::wg_x(), sh);
 }
 
 // ------------------------------------------------------------------ chunk (prefill) MFMA
@@ -2183,13 +2247,28 @@ int64_t decode_grid(int64_t grid_dec) { return (grid_dec + kXcds - 1) / kXcds * 
 
 template <typename T, int G>
 int launch_run(const RunArgs& a, hipStream_t s) {
-  // The combine merges decode and chunk split partials, so it runs last.
-  if (a.app_wgs > 0)
-    hipLaunchKernelGGL((decode_kernel<T, G, true>), dim3((unsigned)(decode_grid(a.grid_dec) * a.hkv + a.app_wgs)),
+  // The combine merges decode and chunk split partials, so it runs last. A second plan's
+  // combine records (a.sc_wgs) follow the decode workgroups of the decode launch, as
+  // 256-thread workgroups like that plan's own combine launch; when this call has no
+  // decode launch, or that plan's rows want 512-thread workgroups, they get a combine
+  // launch of their own first.
+  const bool sc_wide = ceil_div(a.sc_max_k, kSplit) > kCombSmallSplits;
+  const bool sc_in_decode = a.sc_wgs > 0 && a.grid_dec > 0 && !sc_wide;
+  if (a.sc_wgs > 0 && !sc_in_decode) {
+    if (sc_wide)
+      hipLaunchKernelGGL((combine_kernel<T, G, 512>), dim3((unsigned)a.sc_wgs), dim3(512), 0, s, side_combine_args(a));
+    else
+      hipLaunchKernelGGL((combine_kernel<T, G, 256>), dim3((unsigned)a.sc_wgs), dim3(256), 0, s, side_combine_args(a));
+  }
+  const unsigned dec_wgs = (unsigned)(decode_grid(a.grid_dec) * a.hkv);
+  if (sc_in_decode)
+    hipLaunchKernelGGL((decode_kernel<T, G, kExtraCombine>), dim3(dec_wgs + (unsigned)(a.app_wgs + a.sc_wgs)),
                        dim3(kThreads), 0, s, a);
+  else if (a.app_wgs > 0)
+    hipLaunchKernelGGL((decode_kernel<T, G, kExtraAppend>), dim3(dec_wgs + (unsigned)a.app_wgs), dim3(kThreads), 0, s,
+                       a);
   else if (a.grid_dec > 0)
-    hipLaunchKernelGGL((decode_kernel<T, G, false>), dim3((unsigned)(decode_grid(a.grid_dec) * a.hkv)), dim3(kThreads),
-                       0, s, a);
+    hipLaunchKernelGGL((decode_kernel<T, G, kExtraNone>), dim3(dec_wgs), dim3(kThreads), 0, s, a);
   if (a.grid_pf > 0)
     hipLaunchKernelGGL((chunk_kernel<T, G>), dim3((unsigned)(a.grid_pf * a.hkv)), dim3(kChunkThreads), 0, s, a);
   // A cascade merge adds workgroups for its members whose rows have no combine record;
@@ -2386,6 +2465,11 @@ struct MergeSpec {
   const int32_t* part_start;
   const int32_t* part_idx;
   int32_t n_parts;
+  // The level batch's own plan, when this call also runs that plan's combine phase
+  // (level_ws == nullptr: it ran before; level_out / level_lse hold its results).
+  void* level_ws;
+  size_t level_ws_bytes;
+  int32_t level_batch, level_max_q, level_max_k, level_comb_hint;
 };
 
 struct AppendSpec {
@@ -2492,6 +2576,50 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
   a.mg_lse_stride = a.mg_rows = 0;
   a.mg_seq = a.mg_of_seq = a.mg_start = a.mg_idx = nullptr;
   a.mg_members = a.mg_n_idx = 0;
+  a.sc_hdr = nullptr;
+  a.sc_comb_seqs = nullptr;
+  a.sc_part_ml = nullptr;
+  a.sc_part_o = nullptr;
+  a.sc_out = nullptr;
+  a.sc_lse = nullptr;
+  a.sc_o_row = a.sc_o_head = a.sc_dec_cap = a.sc_slot_cap = 0;
+  a.sc_batch = a.sc_max_q = a.sc_max_k = a.sc_total_q = a.sc_grid_comb = a.sc_wgs = 0;
+  if (mg != nullptr && mg->level_ws != nullptr) {
+    // The level plan: same heads and pools, its own workspace, outputs level_out / level_lse
+    // ([level_rows] rows, lse [n_q_heads, level_rows]). Its combine records run in this
+    // call, before the merge reads their rows.
+    if (!tuned_shape(n_q_heads / n_kv_heads, head_dim)) return HX_E_UNSUPPORTED;
+    st = check_shape(mg->level_batch, mg->level_max_q, mg->level_max_k, n_q_heads, n_kv_heads, head_dim);
+    if (st != HX_OK) return st;
+    if (mg->level_rows < 0 || mg->level_rows > INT32_MAX || !mg->level_out || !mg->level_lse)
+      return HX_E_INVALID_ARG;
+    if ((uintptr_t)mg->level_out % 8 || mg->level_row % 4 || mg->level_head % 4 || mg->level_row < 0 ||
+        mg->level_head < 0)
+      return HX_E_INVALID_ARG;
+    const Layout la = make_layout(mg->level_batch, mg->level_max_q, mg->level_max_k, n_q_heads, n_kv_heads);
+    if ((uintptr_t)mg->level_ws % 256 || mg->level_ws_bytes < la.total) return HX_E_WORKSPACE;
+    if (mg->level_batch > 0) {
+      uint8_t* lw = static_cast<uint8_t*>(mg->level_ws);
+      a.sc_hdr = reinterpret_cast<int32_t*>(lw);
+      a.sc_comb_seqs = reinterpret_cast<const int4*>(lw + la.comb_seqs);
+      a.sc_part_ml = reinterpret_cast<float2*>(lw + la.part_ml);
+      a.sc_part_o = reinterpret_cast<uint16_t*>(lw + la.part_o);
+      a.sc_out = static_cast<uint8_t*>(const_cast<void*>(mg->level_out));
+      a.sc_lse = const_cast<float*>(mg->level_lse);
+      a.sc_o_row = mg->level_row;
+      a.sc_o_head = mg->level_head;
+      a.sc_dec_cap = la.max_dec;
+      a.sc_slot_cap = la.max_dec + la.cslot_cap;
+      a.sc_batch = mg->level_batch;
+      a.sc_max_q = mg->level_max_q;
+      a.sc_max_k = mg->level_max_k;
+      a.sc_total_q = (int32_t)mg->level_rows;
+      a.sc_grid_comb = clamp_hint(mg->level_comb_hint, la.max_comb);
+      const int64_t wgs = (int64_t)a.sc_grid_comb * n_kv_heads;
+      if (wgs > INT32_MAX - decode_grid(a.grid_dec) * n_kv_heads - kAppendWGs) return HX_E_INVALID_ARG;
+      a.sc_wgs = (int32_t)wgs;
+    }
+  }
   if (mg != nullptr && mg->n_members > 0) {
     // Tuned shapes only (the merge runs in the combine launch); 16-byte rows for the
     // merged stores and loads; the lse of every row (the unsplit members' merge reads it).
@@ -2653,6 +2781,55 @@ int hx_varlen_attn_run_merged(const void* q, int64_t q_row_stride, int64_t q_hea
   mg.part_start = part_start;
   mg.part_idx = part_idx;
   mg.n_parts = n_parts;
+  mg.level_ws = nullptr;
+  mg.level_ws_bytes = 0;
+  mg.level_batch = mg.level_max_q = mg.level_max_k = mg.level_comb_hint = 0;
+  return run_impl(q, q_row_stride, q_head_stride, nullptr, 0, k_cache, v_cache, kv_row_stride,
+                  kv_head_stride, num_pages, page_size, block_table, block_table_stride, batch,
+                  total_q, max_q, max_k, n_q_heads, n_kv_heads, head_dim, scale, window_left,
+                  window_right, dtype, out, o_row_stride, o_head_stride, lse, decode_items_hint,
+                  prefill_items_hint, combine_seqs_hint, workspace, workspace_bytes, stream, nullptr, &mg);
+}
+
+int hx_varlen_attn_run_cascade(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                               const void* k_cache, const void* v_cache,
+                               int64_t kv_row_stride, int64_t kv_head_stride,
+                               int32_t num_pages, int32_t page_size,
+                               const int32_t* block_table, int32_t block_table_stride,
+                               int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                               int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                               float scale, int32_t window_left, int32_t window_right,
+                               int32_t dtype,
+                               void* out, int64_t o_row_stride, int64_t o_head_stride,
+                               float* lse,
+                               void* level_out, int64_t level_row_stride, int64_t level_head_stride,
+                               float* level_lse, int64_t level_rows,
+                               int32_t level_batch, int32_t level_max_q, int32_t level_max_k,
+                               int32_t level_combine_hint, void* level_workspace, size_t level_workspace_bytes,
+                               const int32_t* member_seq, const int32_t* member_of_seq, int32_t n_members,
+                               const int32_t* part_start, const int32_t* part_idx, int32_t n_parts,
+                               int32_t decode_items_hint, int32_t prefill_items_hint,
+                               int32_t combine_seqs_hint,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  if (n_members < 0 || !level_workspace) return HX_E_INVALID_ARG;
+  MergeSpec mg;
+  mg.level_out = level_out;
+  mg.level_row = level_row_stride;
+  mg.level_head = level_head_stride;
+  mg.level_lse = level_lse;
+  mg.level_rows = level_rows;
+  mg.member_seq = member_seq;
+  mg.member_of_seq = member_of_seq;
+  mg.n_members = n_members;
+  mg.part_start = part_start;
+  mg.part_idx = part_idx;
+  mg.n_parts = n_parts;
+  mg.level_ws = level_workspace;
+  mg.level_ws_bytes = level_workspace_bytes;
+  mg.level_batch = level_batch;
+  mg.level_max_q = level_max_q;
+  mg.level_max_k = level_max_k;
+  mg.level_comb_hint = level_combine_hint;
   return run_impl(q, q_row_stride, q_head_stride, nullptr, 0, k_cache, v_cache, kv_row_stride,
                   kv_head_stride, num_pages, page_size, block_table, block_table_stride, batch,
                   total_q, max_q, max_k, n_q_heads, n_kv_heads, head_dim, scale, window_left,

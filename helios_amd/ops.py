@@ -57,7 +57,12 @@ class MergeParts(NamedTuple):
     is the decode row of sequence ``member_seq[k]`` (``member_of_seq[b]``: sequence b's
     member index or -1); its parts are rows ``part_idx[part_start[k]:part_start[k + 1]]``
     of ``level_out`` ``[A, H, 128]`` with log-sum-exps ``level_lse`` ``[H, A]``. All on the
-    device; the int arrays are contiguous int32."""
+    device; the int arrays are contiguous int32.
+
+    ``level_plan``: the plan that produces ``level_out`` / ``level_lse``, when its run so
+    far covered only its decode and chunk phases (``phases=("decode", "chunk")``, same
+    stream): the merging run then does that plan's combine phase too, in workgroups added
+    to its own decode launch, instead of a launch of its own."""
 
     level_out: torch.Tensor
     level_lse: torch.Tensor
@@ -65,6 +70,7 @@ class MergeParts(NamedTuple):
     member_of_seq: torch.Tensor
     part_start: torch.Tensor
     part_idx: torch.Tensor
+    level_plan: "VarlenAttnPlan | None" = None
 
 
 class AuxRequest(NamedTuple):
@@ -728,12 +734,26 @@ class VarlenAttnPlan:
             n_members = merge.member_seq.numel()
             if merge.part_start.numel() != n_members + 1 or merge.member_of_seq.numel() != self.batch:
                 raise ValueError("merge.part_start needs members + 1 entries and member_of_seq one per sequence.")
-            code = _capi.lib().hx_varlen_attn_run_merged(
-                *common, lo.data_ptr(), lo.stride(0), lo.stride(1), ll.data_ptr(), n_a,
-                merge.member_seq.data_ptr(), merge.member_of_seq.data_ptr(), n_members,
-                merge.part_start.data_ptr(), merge.part_idx.data_ptr(), merge.part_idx.numel(),
-                *hints, self.ws_ptr, self.ws_bytes, _stream_ptr(query.device))
-            _capi.check(code, "hx_varlen_attn_run_merged")
+            lp = merge.level_plan
+            if lp is None:
+                code = _capi.lib().hx_varlen_attn_run_merged(
+                    *common, lo.data_ptr(), lo.stride(0), lo.stride(1), ll.data_ptr(), n_a,
+                    merge.member_seq.data_ptr(), merge.member_of_seq.data_ptr(), n_members,
+                    merge.part_start.data_ptr(), merge.part_idx.data_ptr(), merge.part_idx.numel(),
+                    *hints, self.ws_ptr, self.ws_bytes, _stream_ptr(query.device))
+                _capi.check(code, "hx_varlen_attn_run_merged")
+            else:
+                if not isinstance(lp, VarlenAttnPlan) or lp.device != self.device or lp.n_q_heads != self.n_q_heads \
+                        or lp.n_kv_heads != self.n_kv_heads or lp.head_dim != self.head_dim or lp.total_q != n_a:
+                    raise ValueError("merge.level_plan must be the plan of level_out: same device and heads, "
+                                     "total_q = level_out rows.")
+                code = _capi.lib().hx_varlen_attn_run_cascade(
+                    *common, lo.data_ptr(), lo.stride(0), lo.stride(1), ll.data_ptr(), n_a,
+                    lp.batch, lp.max_q, lp.max_k, lp.hints[2], lp.ws_ptr, lp.ws_bytes,
+                    merge.member_seq.data_ptr(), merge.member_of_seq.data_ptr(), n_members,
+                    merge.part_start.data_ptr(), merge.part_idx.data_ptr(), merge.part_idx.numel(),
+                    *hints, self.ws_ptr, self.ws_bytes, _stream_ptr(query.device))
+                _capi.check(code, "hx_varlen_attn_run_cascade")
         elif query_rows is not None:
             code = _capi.lib().hx_varlen_attn_run_rows(
                 *common[:3], query_rows.data_ptr(), query.shape[0], *common[3:], *hints,

@@ -240,6 +240,42 @@ int hx_varlen_attn_run_merged(const void* q, int64_t q_row_stride, int64_t q_hea
                               void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * hx_varlen_attn_run_merged that also finishes the level batch's own run: the level
+ * plan (level_batch, level_max_q, level_max_k, same heads and head_dim, its workspace
+ * level_workspace) must have run its decode and chunk phases earlier on the same stream,
+ * writing level_out / level_lse ([level_rows] rows, lse [n_q_heads, level_rows]); this
+ * call runs that plan's combine phase (level_combine_hint bounds its records, as
+ * combine_seqs_hint does for a run) before the merge reads the level rows. Its records
+ * run as extra workgroups after the decode workgroups of this call's decode launch;
+ * without a decode launch in this call, or for level rows of more than 8192 keys, they
+ * get a combine launch of their own first. level_out and level_lse end
+ * up with the bits of the level plan's own combine phase, and out / lse with the bits of
+ * hx_varlen_attn_run_merged. Same requirements as hx_varlen_attn_run_merged; level_out
+ * rows need 8-byte alignment (16-byte for the merge, as there). No reference
+ * counterpart: it saves the cascade one dependent launch per layer.
+ */
+int hx_varlen_attn_run_cascade(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                               const void* k_cache, const void* v_cache,
+                               int64_t kv_row_stride, int64_t kv_head_stride,
+                               int32_t num_pages, int32_t page_size,
+                               const int32_t* block_table, int32_t block_table_stride,
+                               int32_t batch, int32_t total_q, int32_t max_q, int32_t max_k,
+                               int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                               float scale, int32_t window_left, int32_t window_right,
+                               int32_t dtype,
+                               void* out, int64_t o_row_stride, int64_t o_head_stride,
+                               float* lse,
+                               void* level_out, int64_t level_row_stride, int64_t level_head_stride,
+                               float* level_lse, int64_t level_rows,
+                               int32_t level_batch, int32_t level_max_q, int32_t level_max_k,
+                               int32_t level_combine_hint, void* level_workspace, size_t level_workspace_bytes,
+                               const int32_t* member_seq, const int32_t* member_of_seq, int32_t n_members,
+                               const int32_t* part_start, const int32_t* part_idx, int32_t n_parts,
+                               int32_t decode_items_hint, int32_t prefill_items_hint,
+                               int32_t combine_seqs_hint,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * KV append + attention in one call: the PagedBatchCache.attend sequence of the
  * reference (paged_cache.py:301-332 and :501-520: _write, i.e. index_copy_ of the new
  * rows into k_cache / v_cache at write_slots, then varlen_attn on the updated pool).

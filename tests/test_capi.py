@@ -33,7 +33,7 @@ def test_loader_rejects_a_library_of_another_abi_version(monkeypatch):
 
 
 def test_abi_version_and_strerror():
-    assert _capi.lib().hx_abi_version() == _capi.ABI_VERSION == 4
+    assert _capi.lib().hx_abi_version() == _capi.ABI_VERSION == 5
     assert _capi.strerror(0) == "success"
     assert "invalid" in _capi.strerror(_capi.HX_E_INVALID_ARG)
     with pytest.raises(ValueError):

@@ -356,3 +356,54 @@ def test_merge_in_the_combine_launch_equals_the_merge_pass(device, always_cascad
             assert torch.equal(got[r], plain[r])
     with pytest.raises(ValueError, match="combine phase"):
         cas.plan_b.run(q, kp, vp, cas.bt_b, return_lse=True, merge=merge, phases=("decode",))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_level_combine_in_the_decode_launch(device, dtype, always_cascade):
+    """``MergeParts(level_plan=plan_a)`` after batch A ran only its decode and chunk
+    phases: batch A's combine records run as extra workgroups of batch B's decode launch,
+    or in a combine launch of their own when the merging call has no decode launch.
+    Either way batch A's rows and log-sum-exps, and batch B's merged out and lse, equal
+    batch A's full run followed by the merging run, bit for bit."""
+    say("level batch's combine in batch B's decode launch", dtype)
+    pool = _pool(device, pages=200, dtype=dtype)
+    cached = [8 * 256 + 5, 8 * 256 + 40, 8 * 256 + 300, 5000, 6100, 3 * 256 + 10, 7000, 2100, 600, 300]
+    _prefix, caches = _shared_caches(pool, cached, prefix_pages=8)
+    batch = PagedBatchCache(caches)
+    batch.prepare(1)
+    cas = batch._cascade
+    assert cas is not None
+    pa, pb = cas.plan_a, cas.plan_b
+    assert pa.hints[2] > 0, pa.hints  # some level rows are split: batch A has combine records
+    g = torch.Generator(device="cpu").manual_seed(11)
+    q = torch.randn((len(caches), 32, 128), generator=g).to(dtype).to(device)
+    kp, vp = pool.keys[0], pool.values[0]
+    rows_a, (_out_rows, part_start, part_idx) = cas.rows_a, cas.merge
+    member_seq, member_of_seq = cas.members
+    o_ref, lse_ref = pa.run(q, kp, vp, cas.bt_a, return_lse=True, query_rows=rows_a)
+    want, want_lse = pb.run(q, kp, vp, cas.bt_b, return_lse=True,
+                            merge=ops.MergeParts(o_ref, lse_ref, member_seq, member_of_seq, part_start, part_idx))
+
+    def level_run():  # batch A without its combine; rows it leaves hold a marker
+        o_a = torch.full_like(o_ref, 7.0)
+        lse_a = torch.full_like(lse_ref, 3.0)
+        pa.run(q, kp, vp, cas.bt_a, out=o_a, lse_out=lse_a, query_rows=rows_a, phases=("decode", "chunk"))
+        return o_a, lse_a, ops.MergeParts(o_a, lse_a, member_seq, member_of_seq, part_start, part_idx, level_plan=pa)
+
+    o_a, lse_a, merge = level_run()
+    got, got_lse = pb.run(q, kp, vp, cas.bt_b, return_lse=True, merge=merge)
+    # The merging call without a decode launch: batch A's records get a launch of their own.
+    o_c, lse_c, merge_c = level_run()
+    out_c = torch.empty_like(want)
+    lse_out_c = torch.empty_like(want_lse)
+    pb.run(q, kp, vp, cas.bt_b, out=out_c, lse_out=lse_out_c, phases=("decode", "chunk"))
+    pb.run(q, kp, vp, cas.bt_b, out=out_c, lse_out=lse_out_c, phases=("combine",), merge=merge_c)
+    torch.cuda.synchronize()
+    assert pa.error_word() == 0 and pb.error_word() == 0
+    for o, lse, out, out_lse in ((o_a, lse_a, got, got_lse), (o_c, lse_c, out_c, lse_out_c)):
+        assert torch.equal(o, o_ref)
+        assert torch.equal(lse, lse_ref)
+        assert torch.equal(out, want)
+        assert torch.equal(out_lse, want_lse)
+    with pytest.raises(ValueError, match="level_plan"):
+        pb.run(q, kp, vp, cas.bt_b, return_lse=True, merge=merge._replace(level_plan=object()))
