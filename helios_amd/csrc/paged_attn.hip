@@ -97,7 +97,7 @@ inline Geometry geometry(int hq, int hkv) {
 }
 
 struct Layout {
-  size_t seq_info, dec_items, comb_seqs, pf_items, pf_base, part_ml, part_o, total;
+  size_t seq_info, dec_items, comb_seqs, pf_items, pf_base, pf_seq, part_ml, part_o, total;
   int64_t max_dec, max_pf, max_comb, cslot_cap;
 };
 
@@ -126,6 +126,7 @@ inline Layout make_layout(int batch, int max_q, int max_k, int hq, int hkv) {
   l.comb_seqs = off; off = align256(off + (size_t)l.max_comb * sizeof(int4));
   l.pf_items = off;  off = align256(off + (size_t)l.max_pf * sizeof(int4));
   l.pf_base = off;   off = align256(off + (size_t)l.max_pf * sizeof(int32_t));
+  l.pf_seq = off;    off = align256(off + (size_t)l.max_pf * sizeof(int4));
   const int64_t slots = l.max_dec + l.cslot_cap;
   l.part_ml = off;   off = align256(off + (size_t)slots * hq * sizeof(float2));
   l.part_o = off;    off = align256(off + (size_t)slots * hq * kD * sizeof(uint16_t));
@@ -257,6 +258,7 @@ struct PlanArgs {
   int4* comb_seqs;
   int4* pf_items;
   int32_t* pf_base;
+  int4* pf_seq;  // per chunk item: its sequence's seq_info entry, read with the item
   int64_t total_k_rows;
   int64_t max_dec, max_pf, max_comb, cslot_cap;
   int32_t batch, total_q, max_q, max_k;
@@ -472,6 +474,7 @@ __device__ void plan_serial(const PlanArgs& a, int* wave_tot, int* err_bits, int
               if (off_p + k < a.max_pf) {
                 a.pf_items[off_p + k] = make_int4(b, row0, hq, fits ? (sp | ((S - 1) << 16)) : 0);
                 a.pf_base[off_p + k] = slot;
+                a.pf_seq[off_p + k] = make_int4(m.q0, m.n, m.L, m.kvb);
               }
             }
           }
@@ -585,6 +588,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
   // Chunk sequence k: its sequence index, first row, clamped (n, L), first flat block, and its item /
   // combine-record / partial-slot offsets once known.
   __shared__ int cs_b[kPlanChunkSeqs], cs_q0[kPlanChunkSeqs], cs_n[kPlanChunkSeqs], cs_L[kPlanChunkSeqs];
+  __shared__ int cs_kvb[kPlanChunkSeqs];
   __shared__ int cs_first[kPlanChunkSeqs + 1];
   __shared__ int cs_off_p[kPlanChunkSeqs], cs_off_c[kPlanChunkSeqs], cs_off_s[kPlanChunkSeqs];
   // Flat block i: key tiles, then (after the split) its offsets within the flat order.
@@ -619,6 +623,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
       cs_q0[k] = m.q0;
       cs_n[k] = m.n;
       cs_L[k] = m.L;
+      cs_kvb[k] = m.kvb;
       cs_first[k] = n_blk + pre.y;
     }
     n_cs += tot.x;
@@ -845,6 +850,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
         if (item0 + j < a.max_pf) {
           a.pf_items[item0 + j] = make_int4(b, row0, hq, fits ? (sp | ((S - 1) << 16)) : 0);
           a.pf_base[item0 + j] = slot;
+          a.pf_seq[item0 + j] = make_int4(cs_q0[k], n, cs_L[k], cs_kvb[k]);
         }
       }
     }
@@ -876,6 +882,7 @@ struct RunArgs {
   const int4* comb_seqs;
   const int4* pf_items;
   const int32_t* pf_base;  // per chunk item: first partial row of its block (split blocks)
+  const int4* pf_seq;      // per chunk item: its sequence's seq_info entry
   float2* part_ml;   // per (slot, head): running max m (log2 units) and sum l
   uint16_t* part_o;  // per (slot, head, dim): o / l in the element type T
   int64_t dec_cap;   // decode slots [0, dec_cap); chunk split rows follow
@@ -1706,6 +1713,9 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   const int g = hx::wg_x() - item * a.hkv;
   const Header hd = read_header(a);
   const int4 it = a.pf_items[item];  // item < grid_pf <= the list's capacity
+  // The item's sequence fields (its seq_info entry, copied by the planner), loaded with
+  // the item instead of after it: one dependent round trip less before the first tile.
+  const int4 si = a.pf_seq[item];
   if (!hd.ok) return;
   const int n_pf = hd.counts.y;
   if (hx::wg_x() == 0 && tid == 0 && n_pf > a.grid_pf) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
@@ -1716,7 +1726,6 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   const int row0 = __builtin_amdgcn_readfirstlane(it.y);
   const int hquad = __builtin_amdgcn_readfirstlane(it.z);
   if ((unsigned)b >= (unsigned)a.batch) return;
-  const int4 si = a.seq_info[b];
   const int q0 = __builtin_amdgcn_readfirstlane(si.x), n = __builtin_amdgcn_readfirstlane(si.y);
   const int L = __builtin_amdgcn_readfirstlane(si.z), kvb = __builtin_amdgcn_readfirstlane(si.w);
   const int off = L - n;  // key position of query row 0
@@ -2429,6 +2438,7 @@ int hx_varlen_attn_plan(const int32_t* cu_seq_q, const int32_t* cu_seq_k,
   a.comb_seqs = reinterpret_cast<int4*>(ws + l.comb_seqs);
   a.pf_items = reinterpret_cast<int4*>(ws + l.pf_items);
   a.pf_base = reinterpret_cast<int32_t*>(ws + l.pf_base);
+  a.pf_seq = reinterpret_cast<int4*>(ws + l.pf_seq);
   a.total_k_rows = total_k_rows;
   a.max_dec = l.max_dec;
   a.max_pf = l.max_pf;
@@ -2531,6 +2541,7 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
   a.comb_seqs = reinterpret_cast<const int4*>(ws + l.comb_seqs);
   a.pf_items = reinterpret_cast<const int4*>(ws + l.pf_items);
   a.pf_base = reinterpret_cast<const int32_t*>(ws + l.pf_base);
+  a.pf_seq = reinterpret_cast<const int4*>(ws + l.pf_seq);
   a.part_ml = reinterpret_cast<float2*>(ws + l.part_ml);
   a.part_o = reinterpret_cast<uint16_t*>(ws + l.part_o);
   a.dec_cap = l.max_dec;

@@ -123,6 +123,8 @@ def layout(batch: int, max_q: int, max_k: int, hq: int, hkv: int) -> dict[str, i
     lay["pf_items"] = off
     off = a256(off + max_pf * 16)
     lay["pf_base"] = off
+    off = a256(off + max_pf * 4)
+    lay["pf_seq"] = off
     lay.update(max_dec=max_dec, max_pf=max_pf, max_comb=max_comb, cslot_cap=cslot)
     return lay
 

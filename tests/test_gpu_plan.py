@@ -46,6 +46,9 @@ def _device_lists(q_lens, k_lens, hq, hkv, window=(-1, 0), page_size=256, device
         words(lay["pf_base"], n_pf),
         words(lay["comb_seqs"], 4 * n_comb).reshape(-1, 4),
     )
+    # Each chunk item carries a copy of its sequence's seq_info entry.
+    pf_seq = words(lay["pf_seq"], 4 * n_pf).reshape(-1, 4)
+    assert np.array_equal(pf_seq, got[0][got[2][:, 0]]) if n_pf else True
     want = plan_model.plan_lists(q_lens, k_lens, hq, hkv, window, lay["max_dec"], lay["cslot_cap"], page_size,
                                  cu_k=cu_k)
     return got, want, err, plan.hints
