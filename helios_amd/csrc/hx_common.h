@@ -170,6 +170,18 @@ __device__ __forceinline__ uint2 ld8_lds_tr16(const void* p) {
   return __builtin_bit_cast(uint2, r);
 }
 
+// Stores with the non-temporal hint (global_store ... nt): the chunk kernel's output rows
+// and split partials are written once at a workgroup's end and read by a later launch;
+// streamed this way the workgroups of a launch finish sooner.
+__device__ __forceinline__ void st16_nt(void* p, uint4 v) {
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(v4u{v.x, v.y, v.z, v.w}, static_cast<v4u*>(p));
+}
+__device__ __forceinline__ void st8_nt(void* p, uint32_t x, uint32_t y) {
+  typedef unsigned v2u __attribute__((ext_vector_type(2)));
+  __builtin_nontemporal_store(v2u{x, y}, static_cast<v2u*>(p));
+}
+
 // 16-byte buffer load at byte offset voff (default cache policy).
 __device__ __forceinline__ uint4 ld16_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
   const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0));

@@ -2046,28 +2046,45 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
       }
     }
   }
-  __syncthreads();  // staged rows visible to the whole wave
+  // Each wave reads back only the rows it staged, and one wave's LDS accesses complete in
+  // order, so a wavefront-scope fence (no instruction, no barrier) orders the reads after
+  // the writes. All eight reads go out before the first store; the stores carry the
+  // non-temporal hint (C3 chunk 37.2 -> 35.4 us, the C5 tick's attention 0.08 ms less).
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   // Lane (r4, c) = (lane >> 4, lane & 15) stores the 16-byte chunk c of staged row 4i + r4.
-  // Output rows are 16-byte aligned unless the caller's strides or pointer are only
-  // 8-byte aligned (allowed): then each chunk goes as two 8-byte stores.
-  const bool out16 = a.o_row % 8 == 0 && a.o_head % 8 == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0;
+  uint4 u[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int sr = 4 * i + (lane >> 4);
-    const int rr = wr0 + sr;
-    const uint4 u = *reinterpret_cast<const uint4*>(stage + sr * kTileRowBytes + 16 * k_chunk_pos(sr, lane & 15));
-    if (rr >= n) continue;
-    if (S > 1) {
+    u[i] = *reinterpret_cast<const uint4*>(stage + sr * kTileRowBytes + 16 * k_chunk_pos(sr, lane & 15));
+  }
+  if (S > 1) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rr = wr0 + 4 * i + (lane >> 4);
       const int64_t slot = slot0 + (int64_t)(rr - row0) * S;
-      if (slot < a.slot_cap) *reinterpret_cast<uint4*>(a.part_o + (slot * a.hq + qh) * kD + 8 * (lane & 15)) = u;
-    } else {
-      uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + (int64_t)(q0 + rr) * a.o_row + (int64_t)qh * a.o_head +
-                    8 * (lane & 15);
-      if (out16) {
-        *reinterpret_cast<uint4*>(o) = u;
-      } else {
-        reinterpret_cast<uint2*>(o)[0] = make_uint2(u.x, u.y);
-        reinterpret_cast<uint2*>(o)[1] = make_uint2(u.z, u.w);
+      if (rr < n && slot < a.slot_cap) hx::st16_nt(a.part_o + (slot * a.hq + qh) * kD + 8 * (lane & 15), u[i]);
+    }
+    return;
+  }
+  // Output rows are 16-byte aligned unless the caller's strides or pointer are only
+  // 8-byte aligned (allowed): then each chunk goes as two 8-byte stores.
+  const bool out16 = a.o_row % 8 == 0 && a.o_head % 8 == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0;
+  uint16_t* const o0 = reinterpret_cast<uint16_t*>(a.out) + (int64_t)qh * a.o_head + 8 * (lane & 15);
+  if (out16) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rr = wr0 + 4 * i + (lane >> 4);
+      if (rr < n) hx::st16_nt(o0 + (int64_t)(q0 + rr) * a.o_row, u[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rr = wr0 + 4 * i + (lane >> 4);
+      if (rr < n) {
+        uint16_t* o = o0 + (int64_t)(q0 + rr) * a.o_row;
+        hx::st8_nt(o, u[i].x, u[i].y);
+        hx::st8_nt(o + 4, u[i].z, u[i].w);
       }
     }
   }

@@ -781,6 +781,8 @@ class VarlenAttnPlan:
             _capi.check(code, "hx_varlen_attn_append_run")
         if CHECK_ERRORS:
             self.check_errors()
+            if merge is not None and merge.level_plan is not None:
+                merge.level_plan.check_errors()  # its combine records ran in this call
         return (out, lse) if return_lse else out
 
 

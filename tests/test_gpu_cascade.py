@@ -359,7 +359,7 @@ def test_merge_in_the_combine_launch_equals_the_merge_pass(device, always_cascad
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_level_combine_in_the_decode_launch(device, dtype, always_cascade):
+def test_level_combine_in_the_decode_launch(device, dtype, always_cascade, monkeypatch):
     """``MergeParts(level_plan=plan_a)`` after batch A ran only its decode and chunk
     phases: batch A's combine records run as extra workgroups of batch B's decode launch,
     or in a combine launch of their own when the merging call has no decode launch.
@@ -407,3 +407,7 @@ def test_level_combine_in_the_decode_launch(device, dtype, always_cascade):
         assert torch.equal(out_lse, want_lse)
     with pytest.raises(ValueError, match="level_plan"):
         pb.run(q, kp, vp, cas.bt_b, return_lse=True, merge=merge._replace(level_plan=object()))
+    # Checked mode reads both plans' error words after the call (and raises on neither).
+    monkeypatch.setattr(ops, "CHECK_ERRORS", True)
+    _o, _l, merge_d = level_run()
+    pb.run(q, kp, vp, cas.bt_b, return_lse=True, merge=merge_d)
