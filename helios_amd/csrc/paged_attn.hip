@@ -1476,7 +1476,7 @@ __device__ __forceinline__ void combine_store(const RunArgs& a, const CombAcc& r
                              hx::pack2_round<T>(r.acc[4] * inv, r.acc[5] * inv), hx::pack2_round<T>(r.acc[6] * inv, r.acc[7] * inv));
   T* orow = reinterpret_cast<T*>(a.out) + (int64_t)row * a.o_row + (int64_t)qh * a.o_head + 8 * ch;
   if (a.o_row % 8 == 0 && a.o_head % 8 == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0) {
-    *reinterpret_cast<uint4*>(orow) = u;
+    hx::st16_nt(orow, u);  // written once, read by a later launch
   } else {
     uint2* o2 = reinterpret_cast<uint2*>(orow);  // rows are 8-byte aligned (checked on the host)
     o2[0] = make_uint2(u.x, u.y);
@@ -1517,7 +1517,7 @@ __device__ __forceinline__ void combine_store_member(const RunArgs& a, const Com
     for (int e = 0; e < 4; ++e) w4[e] = hx::pack2_round<T>(acc[2 * e], acc[2 * e + 1]);
   }
   T* orow = reinterpret_cast<T*>(a.out) + (int64_t)row * a.o_row + (int64_t)qh * a.o_head + 8 * ch;
-  *reinterpret_cast<uint4*>(orow) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+  hx::st16_nt(orow, make_uint4(w4[0], w4[1], w4[2], w4[3]));
   if (a.lse && ch == 0) a.lse[(int64_t)qh * a.total_q + row] = m;
 }
 
