@@ -136,7 +136,9 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_append_vec_kernel(R
       if (!slot_ok) continue;
       const int hv = h - a.hq - a.hkv;
       const uint4 val = *reinterpret_cast<const uint4*>(a.v + row * a.v_row + hv * a.v_head + 8 * j);
-      *reinterpret_cast<uint4*>(a.v_pool + (slot * a.hkv + hv) * kRopeD + 8 * j) = val;
+      // Non-temporal stores here and below: the rows are read by later launches, and
+      // streamed stores finish this one sooner (2048 rows: 11.8-12.0 -> 10.0-10.1 us).
+      hx::st16_nt(a.v_pool + (slot * a.hkv + hv) * kRopeD + 8 * j, val);
       continue;
     }
     const bool is_q = h < a.hq;
@@ -178,7 +180,7 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_append_vec_kernel(R
     }
     uint16_t* dst = is_q ? a.q_out + row * a.qo_row + hh * a.qo_head + 8 * j
                          : a.k_pool + (slot * a.hkv + hh) * kRopeD + 8 * j;
-    *reinterpret_cast<uint4*>(dst) = make_uint4(op[0], op[1], op[2], op[3]);
+    hx::st16_nt(dst, make_uint4(op[0], op[1], op[2], op[3]));
   }
 }
 
