@@ -411,3 +411,54 @@ def test_level_combine_in_the_decode_launch(device, dtype, always_cascade, monke
     monkeypatch.setattr(ops, "CHECK_ERRORS", True)
     _o, _l, merge_d = level_run()
     pb.run(q, kp, vp, cas.bt_b, return_lse=True, merge=merge_d)
+
+
+def test_level_combine_of_long_levels_gets_its_own_launch(device, always_cascade):
+    """Levels longer than 8192 keys (40 shared pages here) want 512-thread combine
+    workgroups, which a decode launch does not hold: batch A's records then get a combine
+    launch of their own inside the merging call. Bits as batch A's full run followed by
+    the merging run."""
+    say("level batch over 40 shared pages: its combine in a launch of its own")
+    config = Qwen3Config(context_length=16384, n_layers=1, dtype=torch.bfloat16)
+    pool = KVPagePool(config, 400, device=device)
+    g = torch.Generator(device=device).manual_seed(13)
+    for t in pool.keys + pool.values:
+        t.normal_(generator=g)
+    prefix = PagedKVCache(pool, 16384)
+    prefix.pages.extend(pool.acquire(40))
+    prefix.length = 40 * 256
+    caches = []
+    for n in [40 * 256 + 7, 40 * 256 + 300, 41 * 256 + 5, 44 * 256, 38 * 256 + 9, 12000]:
+        cache = PagedKVCache(pool, 16384)
+        shared = min(40, n // 256)
+        cache.pages.extend(prefix.pages[:shared])
+        cache.pages.extend(pool.acquire(-(-n // 256) - shared))
+        cache.length = n
+        caches.append(cache)
+    batch = PagedBatchCache(caches)
+    batch.prepare(1)
+    cas = batch._cascade
+    assert cas is not None
+    pa, pb = cas.plan_a, cas.plan_b
+    assert pa.max_k > 8192 and pa.hints[2] > 0, (pa.max_k, pa.hints)
+    q = torch.randn((len(caches), 32, 128), generator=torch.Generator(device="cpu").manual_seed(5)).to(
+        torch.bfloat16).to(device)
+    kp, vp = pool.keys[0], pool.values[0]
+    rows_a, (_out_rows, part_start, part_idx) = cas.rows_a, cas.merge
+    member_seq, member_of_seq = cas.members
+    o_ref, lse_ref = pa.run(q, kp, vp, cas.bt_a, return_lse=True, query_rows=rows_a)
+    want, want_lse = pb.run(q, kp, vp, cas.bt_b, return_lse=True,
+                            merge=ops.MergeParts(o_ref, lse_ref, member_seq, member_of_seq, part_start, part_idx))
+    o_a = torch.full_like(o_ref, 7.0)
+    lse_a = torch.full_like(lse_ref, 3.0)
+    pa.run(q, kp, vp, cas.bt_a, out=o_a, lse_out=lse_a, query_rows=rows_a, phases=("decode", "chunk"))
+    got, got_lse = pb.run(q, kp, vp, cas.bt_b, return_lse=True,
+                          merge=ops.MergeParts(o_a, lse_a, member_seq, member_of_seq, part_start, part_idx,
+                                               level_plan=pa))
+    torch.cuda.synchronize()
+    assert pa.error_word() == 0 and pb.error_word() == 0
+    assert torch.equal(o_a, o_ref) and torch.equal(lse_a, lse_ref)
+    assert torch.equal(got, want) and torch.equal(got_lse, want_lse)
+    # And the attend path itself against the oracle.
+    out = cas.attend(q, kp, vp)
+    _compare(out.float().cpu().numpy(), _oracle(pool, caches, [1] * len(caches), q), "cascade attend, 40-page levels")
