@@ -178,6 +178,30 @@ def test_attention_entry_points_reject_bad_arguments_on_the_host():
     assert lib.hx_kv_gather(16, 4, 256, 8, 128, 2, 16, 1, 257, 16, None) == _capi.HX_E_INVALID_ARG
 
 
+def test_cascade_run_rejects_a_bad_level_plan_on_the_host():
+    """hx_varlen_attn_run_cascade checks the level plan's workspace and rows before any
+    launch or device access (the pointers below are never dereferenced): a missing level
+    workspace, one that is misaligned or too small for the level shape, and level rows
+    that are not 8-byte aligned are refused."""
+    lib = _capi.lib()
+    mib = 1 << 20
+
+    def call(level_out=64 * mib, level_ws=128 * mib, level_ws_bytes=1 << 30):
+        return lib.hx_varlen_attn_run_cascade(
+            16 * mib, 4096, 128, 32 * mib, 48 * mib, 1024, 128, 16, 256, 8 * mib, 4,
+            2, 2, 1, 512, 32, 8, 128, 1 / math.sqrt(128), -1, 0, _capi.HX_DTYPE_BF16,
+            96 * mib, 4096, 128, 112 * mib,
+            level_out, 4096, 128, 120 * mib, 2,
+            1, 2, 512, -1, level_ws, level_ws_bytes,
+            121 * mib, 122 * mib, 1, 123 * mib, 124 * mib, 1,
+            -1, -1, -1, 256 * mib, 1 << 30, None)
+
+    assert call(level_ws=None) == _capi.HX_E_INVALID_ARG
+    assert call(level_ws=128 * mib + 8) == _capi.HX_E_WORKSPACE
+    assert call(level_ws_bytes=16) == _capi.HX_E_WORKSPACE
+    assert call(level_out=64 * mib + 4) == _capi.HX_E_INVALID_ARG
+
+
 def test_noalloc_rejects_a_tick_beyond_its_scratch():
     """hx_varlen_attn_noalloc checks the shape against its scratch array before it touches
     the device: a tick whose workspace exceeds HX_NOALLOC_SCRATCH_BYTES (128 MiB) returns
