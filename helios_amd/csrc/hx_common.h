@@ -182,6 +182,21 @@ __device__ __forceinline__ void st8_nt(void* p, uint32_t x, uint32_t y) {
   __builtin_nontemporal_store(v2u{x, y}, static_cast<v2u*>(p));
 }
 
+// Holds a loaded value in registers at this point of the program, so that the
+// compiler cannot sink its load below a later branch (a load issued before a test
+// shares the memory round trip of the loads the test waits for).
+template <typename W>
+__device__ __forceinline__ void hold(const W& v) {
+  if constexpr (sizeof(W) >= 4) {
+    struct Words { uint32_t d[sizeof(W) / 4]; };
+    const Words u = __builtin_bit_cast(Words, v);
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(W) / 4); ++i) asm volatile("" ::"v"(u.d[i]));
+  } else {
+    asm volatile("" ::"v"((uint32_t)v));
+  }
+}
+
 // 16-byte buffer load at byte offset voff (default cache policy).
 __device__ __forceinline__ uint4 ld16_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
   const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0));

@@ -24,23 +24,47 @@ struct AppendArgs {
   int32_t head_b;   // bytes of one head row (head_dim * elem_bytes)
   int32_t words;    // words of type W per head row
   int32_t n_wg;     // workgroups of the launch (the grid stride is n_wg * 256 threads)
+  int32_t lw, lh;   // log2 of words and n_kv (the shift form only)
 };
 
-template <typename W>
+// Each thread moves one word of one head row. The slot, K and V loads of an iteration
+// are all issued before the slot is tested (the new rows are always in range), so the
+// iteration waits for memory once before its stores, not twice. SHIFT is the form for
+// head rows of 2^lw words and 2^lh KV heads with every index and source offset below
+// 2^31: the thread index splits by shifts and masks in 32-bit arithmetic.
+template <typename W, bool SHIFT>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   const int64_t per_token = (int64_t)a.n_kv * a.words;
   const int64_t total = a.n_tokens * per_token;
   const int64_t pool_row_b = (int64_t)a.n_kv * a.head_b;
   for (int64_t idx = (int64_t)hx::wg_x() * 256 + hx::tid_x(); idx < total; idx += (int64_t)a.n_wg * 256) {
-    const int64_t t = idx / per_token;
-    const int rem = (int)(idx - t * per_token);
-    const int h = rem / a.words;
-    const int w = rem - h * a.words;
+    int64_t t;
+    int h, w;
+    const uint8_t* ks;
+    const uint8_t* vs;
+    if constexpr (SHIFT) {
+      const int i = (int)idx;
+      w = i & ((1 << a.lw) - 1);
+      h = (i >> a.lw) & ((1 << a.lh) - 1);
+      const int ti = i >> (a.lw + a.lh);
+      t = ti;
+      ks = a.k + (uint32_t)(ti * (int)a.k_row_b + h * (int)a.k_head_b);
+      vs = a.v + (uint32_t)(ti * (int)a.v_row_b + h * (int)a.v_head_b);
+    } else {
+      t = idx / per_token;
+      const int rem = (int)(idx - t * per_token);
+      h = rem / a.words;
+      w = rem - h * a.words;
+      ks = a.k + t * a.k_row_b + h * a.k_head_b;
+      vs = a.v + t * a.v_row_b + h * a.v_head_b;
+    }
     const int64_t slot = a.slots[t];
+    const W kw = reinterpret_cast<const W*>(ks)[w];
+    const W vw = reinterpret_cast<const W*>(vs)[w];
+    hx::hold(kw);
+    hx::hold(vw);
     if (slot < 0 || slot >= a.pool_rows) continue;
     const int64_t dst = slot * pool_row_b + (int64_t)h * a.head_b;
-    const W kw = reinterpret_cast<const W*>(a.k + t * a.k_row_b + h * a.k_head_b)[w];
-    const W vw = reinterpret_cast<const W*>(a.v + t * a.v_row_b + h * a.v_head_b)[w];
     if constexpr (sizeof(W) == 16) {
       // Non-temporal stores: the rows are read back by a later launch, and streamed
       // stores finish the launch sooner (2048 rows: 3.4-3.6 -> 3.0-3.1 us).
@@ -250,15 +274,29 @@ int hx_kv_append(void* k_pool, void* v_pool, int64_t pool_rows,
                                  (uint64_t)(uintptr_t)k_pool, (uint64_t)(uintptr_t)v_pool,
                                  (uint64_t)(uintptr_t)k_new, (uint64_t)(uintptr_t)v_new});
   a.words = a.head_b / wb;
-  const int grid = grid_for(n_tokens * n_kv_heads * (int64_t)a.words, 256);
+  const int64_t items = n_tokens * n_kv_heads * (int64_t)a.words;
+  const int grid = grid_for(items, 256);
   a.n_wg = grid;
+  a.lw = 0;
+  a.lh = 0;
+  while ((1 << a.lw) < a.words) ++a.lw;
+  while ((1 << a.lh) < n_kv_heads) ++a.lh;
+  const int64_t lim = (int64_t)1 << 31;
+  auto fits = [&](int64_t row_b, int64_t head_b) {
+    return row_b >= 0 && head_b >= 0 && n_tokens * row_b + (int64_t)n_kv_heads * head_b < lim;
+  };
+  const bool shift = (1 << a.lw) == a.words && (1 << a.lh) == n_kv_heads && items + (int64_t)grid * 256 < lim &&
+                     fits(a.k_row_b, a.k_head_b) && fits(a.v_row_b, a.v_head_b);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (wb) {
-    case 16: hipLaunchKernelGGL(kv_append_kernel<uint4>, dim3(grid), dim3(256), 0, s, a); break;
-    case 8: hipLaunchKernelGGL(kv_append_kernel<uint2>, dim3(grid), dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(kv_append_kernel<uint32_t>, dim3(grid), dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(kv_append_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL(kv_append_kernel<uint8_t>, dim3(grid), dim3(256), 0, s, a); break;
+    case 16:
+      if (shift) hipLaunchKernelGGL((kv_append_kernel<uint4, true>), dim3(grid), dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((kv_append_kernel<uint4, false>), dim3(grid), dim3(256), 0, s, a);
+      break;
+    case 8: hipLaunchKernelGGL((kv_append_kernel<uint2, false>), dim3(grid), dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((kv_append_kernel<uint32_t, false>), dim3(grid), dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((kv_append_kernel<uint16_t, false>), dim3(grid), dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((kv_append_kernel<uint8_t, false>), dim3(grid), dim3(256), 0, s, a); break;
   }
   return hx::status_from_hip(hipGetLastError());
 }

@@ -72,6 +72,32 @@ def test_append_from_strided_views_and_page_boundaries(device):
     assert not k_pool.view(-1, H, D)[mask].any()
 
 
+@pytest.mark.parametrize("dtype,heads,dim", [
+    (torch.bfloat16, 3, 128),   # 16-byte words, 3 heads: the division form
+    (torch.bfloat16, 8, 96),    # 12 words per head row: the division form
+    (torch.float32, 2, 6),      # 8-byte words
+    (torch.float16, 4, 64),     # 8 words, 4 heads: the shift form
+])
+def test_append_other_head_shapes(device, dtype, heads, dim):
+    say("append shape", dtype, heads, dim)
+    P, S, T = 3, 256, 301
+    k_pool = random_bits((P, S, heads, dim), dtype, device, 11)
+    v_pool = random_bits((P, S, heads, dim), dtype, device, 12)
+    k_new = random_bits((T, heads, dim), dtype, device, 13)
+    v_new = random_bits((T, heads, dim), dtype, device, 14)
+    slots = torch.randperm(P * S, generator=torch.Generator().manual_seed(15))[:T]
+    slots[7], slots[100] = -1, P * S  # skipped rows
+    slots = slots.to(device)
+    keep = (slots >= 0) & (slots < P * S)
+    ek, ev = bits(k_pool).clone().view(-1, heads, dim), bits(v_pool).clone().view(-1, heads, dim)
+    ek.index_copy_(0, slots[keep], bits(k_new)[keep])
+    ev.index_copy_(0, slots[keep], bits(v_new)[keep])
+    ops.kv_append(k_pool, v_pool, slots, k_new, v_new)
+    torch.cuda.synchronize()
+    assert torch.equal(bits(k_pool).view(-1, heads, dim), ek)
+    assert torch.equal(bits(v_pool).view(-1, heads, dim), ev)
+
+
 def test_append_skips_out_of_range_slots_and_empty(device):
     say("append out-of-range slots")
     P, S, H, D = 2, 256, 8, 128
