@@ -13,7 +13,7 @@ HEADER_PATH = Path(__file__).resolve().parent.parent / "include" / "helios_paged
 
 HX_OK = 0
 # hx_abi_version() of the library these signatures describe (bumped on any signature change).
-ABI_VERSION = 5
+ABI_VERSION = 6
 HX_E_INVALID_ARG = -1
 HX_E_UNSUPPORTED = -2
 HX_E_WORKSPACE = -3
@@ -124,6 +124,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_void_p, _i64, _i64, _c_void_p, _i64,
          _i32, _i32, _i32,
          _i32, _c_void_p, _size,
+         _c_void_p, _i32, _c_void_p, _i64, _i32, _i32, _i32,
          _c_void_p, _c_void_p, _i32,
          _c_void_p, _c_void_p, _i32,
          _i32, _i32, _i32,

@@ -243,7 +243,7 @@ const char* hx_strerror(int code) {
   return "unknown helios_paged status";
 }
 
-int hx_abi_version(void) { return 5; }
+int hx_abi_version(void) { return 6; }
 
 int hx_kv_append(void* k_pool, void* v_pool, int64_t pool_rows,
                  const void* k_new, int64_t k_row_stride, int64_t k_head_stride,

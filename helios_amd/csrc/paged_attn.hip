@@ -984,7 +984,7 @@ struct Header {
   int4 counts;  // H_NDEC, H_NPF, H_NCOMB, H_ERR
   bool ok;
 };
-__device__ __forceinline__ Header read_header(const RunArgs& a) {
+__device__ __forceinline__ Header read_header(const RunArgs& a, int wg) {
   const int4 h0 = *reinterpret_cast<const int4*>(a.hdr);
   const int4 h1 = *reinterpret_cast<const int4*>(a.hdr + 4);
   const int2 h2 = *reinterpret_cast<const int2*>(a.hdr + 8);
@@ -992,9 +992,10 @@ __device__ __forceinline__ Header read_header(const RunArgs& a) {
   r.counts = h0;
   r.ok = (h2.y == kPlanStamp) & (h1.x == a.batch) & (h1.y == a.max_q) & (h1.z == a.max_k) &
          (h1.w == a.hq) & (h2.x == a.hkv);
-  if (!r.ok && hx::wg_x() == 0 && hx::tid_x() == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_PLAN_MISMATCH);
+  if (!r.ok && wg == 0 && hx::tid_x() == 0) atomicOr(&a.hdr[H_ERR], HX_WERR_PLAN_MISMATCH);
   return r;
 }
+__device__ __forceinline__ Header read_header(const RunArgs& a) { return read_header(a, hx::wg_x()); }
 
 template <typename T>
 __device__ __forceinline__ uint4 ld16(const T* p) {
@@ -1697,8 +1698,11 @@ __device__ __forceinline__ int v_chunk_pos(int r, int c) { return c ^ (2 * (r & 
 // every LDS access names its buffer variable statically: the compiler then knows that
 // the copies in flight (into the other buffer) do not alias the reads, and adds no wait
 // for them. Two waves per SIMD hide each other's LDS and memory latency.
+// The body of one workgroup: work item and KV head from workgroup index wg of a's items.
+// side: a is the second plan of a paired launch (chunk_pair_kernel). Both copies of the
+// body in that launch share one set of LDS tiles.
 template <typename T, int G>
-__global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
+__device__ __forceinline__ void chunk_body(const RunArgs& a, const int wg, const bool side) {
   typedef hx::Elem<T> E;
   typedef typename E::v8 v8;
   constexpr int Gw = G < 4 ? G : 4;
@@ -1709,16 +1713,19 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
 
   const int tid = hx::tid_x(), lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, held in a scalar register
-  const int item = hx::wg_x() / a.hkv;
-  const int g = hx::wg_x() - item * a.hkv;
-  const Header hd = read_header(a);
+  const int item = wg / a.hkv;
+  const int g = wg - item * a.hkv;
+  const Header hd = read_header(a, wg);
   const int4 it = a.pf_items[item];  // item < grid_pf <= the list's capacity
   // The item's sequence fields (its seq_info entry, copied by the planner), loaded with
   // the item instead of after it: one dependent round trip less before the first tile.
   const int4 si = a.pf_seq[item];
   if (!hd.ok) return;
   const int n_pf = hd.counts.y;
-  if (hx::wg_x() == 0 && tid == 0 && n_pf > a.grid_pf) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
+  if (wg == 0 && tid == 0 && n_pf > a.grid_pf) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
+  // The level batch of a paired launch has no decode launch in this call: decode items in
+  // its plan would be left unwritten.
+  if (side && wg == 0 && tid == 0 && hd.counts.x > 0) atomicOr(&a.hdr[H_ERR], HX_WERR_GRID);
   if (item >= n_pf) return;
   // Work-item and sequence fields are workgroup-uniform: keep them (and the tile loop
   // they bound) in scalar registers.
@@ -2090,6 +2097,25 @@ __global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
   }
 }
 
+template <typename T, int G>
+__global__ __launch_bounds__(kChunkThreads, 2) void chunk_kernel(RunArgs a) {
+  chunk_body<T, G>(a, hx::wg_x(), false);
+}
+
+// One launch for two plans' chunk items (a cascade's batch and its level batch, run in
+// one call): workgroups [0, a0.grid_pf * hkv) take a0's items, the rest a1's, each
+// through its own copy of the body, which reads that plan's arguments directly. a0's
+// come first, so the level batch's short items fill the tail of a0's round.
+template <typename T, int G>
+__global__ __launch_bounds__(kChunkThreads, 2) void chunk_pair_kernel(RunArgs a0, RunArgs a1) {
+  const int n0 = a0.grid_pf * a0.hkv;
+  const int wg = hx::wg_x();
+  if (wg < n0)
+    chunk_body<T, G>(a0, wg, false);
+  else
+    chunk_body<T, G>(a1, wg - n0, true);
+}
+
 // ------------------------------------------------------------------ any head_dim
 // Attention for shapes the tuned kernels do not cover: head_dim any multiple of 8 up to
 // 256, and any group size G. One workgroup per (sequence, block of query rows, KV head
@@ -2272,7 +2298,14 @@ bool valid_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
 int64_t decode_grid(int64_t grid_dec) { return (grid_dec + kXcds - 1) / kXcds * kXcds; }
 
 template <typename T, int G>
-int launch_run(const RunArgs& a, hipStream_t s) {
+int launch_run(const RunArgs& a, const RunArgs* side_pf, hipStream_t s) {
+  // A second plan's chunk items (side_pf: a cascade's level batch, run in this call) share
+  // one chunk launch with this plan's, first: the level batch's combine records below read
+  // its partials. This call then appends nothing, so this plan's chunk rows need no
+  // decode launch before them.
+  if (side_pf != nullptr && (a.grid_pf > 0 || side_pf->grid_pf > 0))
+    hipLaunchKernelGGL((chunk_pair_kernel<T, G>), dim3((unsigned)((a.grid_pf + side_pf->grid_pf) * a.hkv)),
+                       dim3(kChunkThreads), 0, s, a, *side_pf);
   // The combine merges decode and chunk split partials, so it runs last. A second plan's
   // combine records (a.sc_wgs) follow the decode workgroups of the decode launch, as
   // 256-thread workgroups like that plan's own combine launch; when this call has no
@@ -2295,7 +2328,7 @@ int launch_run(const RunArgs& a, hipStream_t s) {
                        a);
   else if (a.grid_dec > 0)
     hipLaunchKernelGGL((decode_kernel<T, G, kExtraNone>), dim3(dec_wgs), dim3(kThreads), 0, s, a);
-  if (a.grid_pf > 0)
+  if (a.grid_pf > 0 && side_pf == nullptr)
     hipLaunchKernelGGL((chunk_kernel<T, G>), dim3((unsigned)(a.grid_pf * a.hkv)), dim3(kChunkThreads), 0, s, a);
   // A cascade merge adds workgroups for its members whose rows have no combine record;
   // it runs in this launch whenever it is given (the call that holds the combine phase).
@@ -2312,12 +2345,12 @@ int launch_run(const RunArgs& a, hipStream_t s) {
 }
 
 template <typename T>
-int launch_run_g(const RunArgs& a, int G, hipStream_t s) {
+int launch_run_g(const RunArgs& a, const RunArgs* side_pf, int G, hipStream_t s) {
   switch (G) {
-    case 1: return launch_run<T, 1>(a, s);
-    case 2: return launch_run<T, 2>(a, s);
-    case 4: return launch_run<T, 4>(a, s);
-    case 8: return launch_run<T, 8>(a, s);
+    case 1: return launch_run<T, 1>(a, side_pf, s);
+    case 2: return launch_run<T, 2>(a, side_pf, s);
+    case 4: return launch_run<T, 4>(a, side_pf, s);
+    case 8: return launch_run<T, 8>(a, side_pf, s);
     default: return HX_E_UNSUPPORTED;
   }
 }
@@ -2497,6 +2530,14 @@ struct MergeSpec {
   void* level_ws;
   size_t level_ws_bytes;
   int32_t level_batch, level_max_q, level_max_k, level_comb_hint;
+  // The level batch's chunk phase too, in this call's chunk launch (level_bt == nullptr:
+  // it ran before): its block table, query row map and chunk-item hint.
+  const int32_t* level_bt;
+  int32_t level_bt_stride;
+  const int64_t* level_q_rows;
+  int64_t level_q_rows_total;
+  int32_t level_pf_hint;
+  int32_t level_win_left, level_win_right;
 };
 
 struct AppendSpec {
@@ -2612,6 +2653,8 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
   a.sc_lse = nullptr;
   a.sc_o_row = a.sc_o_head = a.sc_dec_cap = a.sc_slot_cap = 0;
   a.sc_batch = a.sc_max_q = a.sc_max_k = a.sc_total_q = a.sc_grid_comb = a.sc_wgs = 0;
+  RunArgs side_pf;
+  bool has_side_pf = false;
   if (mg != nullptr && mg->level_ws != nullptr) {
     // The level plan: same heads and pools, its own workspace, outputs level_out / level_lse
     // ([level_rows] rows, lse [n_q_heads, level_rows]). Its combine records run in this
@@ -2646,6 +2689,48 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
       const int64_t wgs = (int64_t)a.sc_grid_comb * n_kv_heads;
       if (wgs > INT32_MAX - decode_grid(a.grid_dec) * n_kv_heads - kAppendWGs) return HX_E_INVALID_ARG;
       a.sc_wgs = (int32_t)wgs;
+    }
+    if (mg->level_bt != nullptr && mg->level_batch > 0) {
+      // The level plan's chunk items in this call's chunk launch: the same pools, heads
+      // and scale, its own window, block table, row map, workspace and outputs. That
+      // launch comes first (the level's combine records read its partials), so this call
+      // appends nothing.
+      if (app != nullptr) return HX_E_INVALID_ARG;
+      if (page_size > 0 && mg->level_bt_stride < 1) return HX_E_INVALID_ARG;
+      if (!mg->level_q_rows || mg->level_q_rows_total < 0) return HX_E_INVALID_ARG;
+      uint8_t* lw = static_cast<uint8_t*>(mg->level_ws);
+      side_pf = a;
+      side_pf.out = static_cast<uint8_t*>(const_cast<void*>(mg->level_out));
+      side_pf.lse = const_cast<float*>(mg->level_lse);
+      side_pf.o_row = mg->level_row;
+      side_pf.o_head = mg->level_head;
+      side_pf.bt = mg->level_bt;
+      side_pf.bt_stride = mg->level_bt_stride;
+      side_pf.hdr = reinterpret_cast<int32_t*>(lw);
+      side_pf.seq_info = reinterpret_cast<const int4*>(lw + la.seq_info);
+      side_pf.dec_items = reinterpret_cast<const int4*>(lw + la.dec_items);
+      side_pf.comb_seqs = reinterpret_cast<const int4*>(lw + la.comb_seqs);
+      side_pf.pf_items = reinterpret_cast<const int4*>(lw + la.pf_items);
+      side_pf.pf_base = reinterpret_cast<const int32_t*>(lw + la.pf_base);
+      side_pf.pf_seq = reinterpret_cast<const int4*>(lw + la.pf_seq);
+      side_pf.part_ml = reinterpret_cast<float2*>(lw + la.part_ml);
+      side_pf.part_o = reinterpret_cast<uint16_t*>(lw + la.part_o);
+      side_pf.dec_cap = la.max_dec;
+      side_pf.slot_cap = la.max_dec + la.cslot_cap;
+      side_pf.batch = mg->level_batch;
+      side_pf.max_q = mg->level_max_q;
+      side_pf.max_k = mg->level_max_k;
+      side_pf.total_q = (int32_t)mg->level_rows;
+      side_pf.grid_dec = 0;
+      side_pf.grid_pf = mg->level_max_q >= 2 ? clamp_hint(mg->level_pf_hint, la.max_pf) : 0;
+      side_pf.grid_comb = 0;
+      side_pf.win_left = mg->level_win_left;
+      side_pf.win_right = mg->level_win_right;
+      side_pf.q_rows = mg->level_q_rows;
+      side_pf.q_rows_total = mg->level_q_rows_total;
+      side_pf.sc_wgs = 0;
+      if (((int64_t)a.grid_pf + side_pf.grid_pf) * n_kv_heads > INT32_MAX) return HX_E_INVALID_ARG;
+      has_side_pf = true;
     }
   }
   if (mg != nullptr && mg->n_members > 0) {
@@ -2725,8 +2810,9 @@ int run_impl(const void* q, int64_t q_row_stride, int64_t q_head_stride,
     if (dtype == HX_DTYPE_BF16) return launch_generic<__bf16>(a, gs, s);
     return launch_generic<_Float16>(a, gs, s);
   }
-  if (dtype == HX_DTYPE_BF16) return launch_run_g<__bf16>(a, G, s);
-  return launch_run_g<_Float16>(a, G, s);
+  const RunArgs* side = has_side_pf ? &side_pf : nullptr;
+  if (dtype == HX_DTYPE_BF16) return launch_run_g<__bf16>(a, side, G, s);
+  return launch_run_g<_Float16>(a, side, G, s);
 }
 
 }  // namespace
@@ -2812,6 +2898,12 @@ int hx_varlen_attn_run_merged(const void* q, int64_t q_row_stride, int64_t q_hea
   mg.level_ws = nullptr;
   mg.level_ws_bytes = 0;
   mg.level_batch = mg.level_max_q = mg.level_max_k = mg.level_comb_hint = 0;
+  mg.level_bt = nullptr;
+  mg.level_bt_stride = 0;
+  mg.level_q_rows = nullptr;
+  mg.level_q_rows_total = 0;
+  mg.level_pf_hint = 0;
+  mg.level_win_left = mg.level_win_right = -1;
   return run_impl(q, q_row_stride, q_head_stride, nullptr, 0, k_cache, v_cache, kv_row_stride,
                   kv_head_stride, num_pages, page_size, block_table, block_table_stride, batch,
                   total_q, max_q, max_k, n_q_heads, n_kv_heads, head_dim, scale, window_left,
@@ -2834,6 +2926,9 @@ int hx_varlen_attn_run_cascade(const void* q, int64_t q_row_stride, int64_t q_he
                                float* level_lse, int64_t level_rows,
                                int32_t level_batch, int32_t level_max_q, int32_t level_max_k,
                                int32_t level_combine_hint, void* level_workspace, size_t level_workspace_bytes,
+                               const int32_t* level_block_table, int32_t level_block_table_stride,
+                               const int64_t* level_query_rows, int64_t level_query_rows_total,
+                               int32_t level_prefill_hint, int32_t level_window_left, int32_t level_window_right,
                                const int32_t* member_seq, const int32_t* member_of_seq, int32_t n_members,
                                const int32_t* part_start, const int32_t* part_idx, int32_t n_parts,
                                int32_t decode_items_hint, int32_t prefill_items_hint,
@@ -2858,6 +2953,13 @@ int hx_varlen_attn_run_cascade(const void* q, int64_t q_row_stride, int64_t q_he
   mg.level_max_q = level_max_q;
   mg.level_max_k = level_max_k;
   mg.level_comb_hint = level_combine_hint;
+  mg.level_bt = level_block_table;
+  mg.level_bt_stride = level_block_table_stride;
+  mg.level_q_rows = level_query_rows;
+  mg.level_q_rows_total = level_query_rows_total;
+  mg.level_pf_hint = level_prefill_hint;
+  mg.level_win_left = level_window_left;
+  mg.level_win_right = level_window_right;
   return run_impl(q, q_row_stride, q_head_stride, nullptr, 0, k_cache, v_cache, kv_row_stride,
                   kv_head_stride, num_pages, page_size, block_table, block_table_stride, batch,
                   total_q, max_q, max_k, n_q_heads, n_kv_heads, head_dim, scale, window_left,

@@ -62,7 +62,13 @@ class MergeParts(NamedTuple):
     ``level_plan``: the plan that produces ``level_out`` / ``level_lse``, when its run so
     far covered only its decode and chunk phases (``phases=("decode", "chunk")``, same
     stream): the merging run then does that plan's combine phase too, in workgroups added
-    to its own decode launch, instead of a launch of its own."""
+    to its own decode launch, instead of a launch of its own.
+
+    ``level_block_table`` (and ``level_query_rows``, int64 rows of the merging run's
+    query): the level plan has not run at all and holds no decode rows; the merging run
+    (all three phases, no append) runs its chunk items too, in one chunk launch with its
+    own, ahead of its decode launch. ``level_out`` / ``level_lse`` are then outputs of
+    that run (any contents on entry)."""
 
     level_out: torch.Tensor
     level_lse: torch.Tensor
@@ -71,6 +77,8 @@ class MergeParts(NamedTuple):
     part_start: torch.Tensor
     part_idx: torch.Tensor
     level_plan: "VarlenAttnPlan | None" = None
+    level_block_table: torch.Tensor | None = None
+    level_query_rows: torch.Tensor | None = None
 
 
 class AuxRequest(NamedTuple):
@@ -747,9 +755,30 @@ class VarlenAttnPlan:
                         or lp.n_kv_heads != self.n_kv_heads or lp.head_dim != self.head_dim or lp.total_q != n_a:
                     raise ValueError("merge.level_plan must be the plan of level_out: same device and heads, "
                                      "total_q = level_out rows.")
+                lbt, lrows = merge.level_block_table, merge.level_query_rows
+                if lbt is None and lrows is not None:
+                    raise ValueError("merge.level_query_rows needs merge.level_block_table.")
+                if lbt is not None:
+                    # The level plan's chunk items run in this call (see MergeParts).
+                    if set(phases) != {"decode", "chunk", "combine"}:
+                        raise ValueError("a merge that runs the level plan's chunk items needs all three phases.")
+                    if lp.hints[0] != 0 or lp.page_size != self.page_size:
+                        raise ValueError("merge.level_plan must hold no decode rows and share the page size to "
+                                         "run in this call.")
+                    if lp.page_size > 0 and (lbt.dtype != torch.int32 or lbt.ndim != 2 or lbt.shape[0] != lp.batch
+                                             or lbt.shape[1] != lp.block_table_stride or lbt.stride(1) != 1
+                                             or lbt.stride(0) != lp.block_table_stride or lbt.device != self.device):
+                        raise ValueError("merge.level_block_table must be the level plan's row-contiguous int32 "
+                                         "[batch, width] table on the device.")
+                    if lrows is None or lrows.dtype != torch.int64 or lrows.ndim != 1 or not lrows.is_contiguous() \
+                            or lrows.numel() != lp.total_q or lrows.device != self.device:
+                        raise ValueError("merge.level_query_rows must be contiguous int64 [level rows] on the device.")
+                level_chunk = (None, 0, None, 0, 0, -1, -1) if lbt is None else (
+                    lbt.data_ptr(), lp.block_table_stride, lrows.data_ptr(), query.shape[0], lp.hints[1],
+                    lp.window[0], lp.window[1])
                 code = _capi.lib().hx_varlen_attn_run_cascade(
                     *common, lo.data_ptr(), lo.stride(0), lo.stride(1), ll.data_ptr(), n_a,
-                    lp.batch, lp.max_q, lp.max_k, lp.hints[2], lp.ws_ptr, lp.ws_bytes,
+                    lp.batch, lp.max_q, lp.max_k, lp.hints[2], lp.ws_ptr, lp.ws_bytes, *level_chunk,
                     merge.member_seq.data_ptr(), merge.member_of_seq.data_ptr(), n_members,
                     merge.part_start.data_ptr(), merge.part_idx.data_ptr(), merge.part_idx.numel(),
                     *hints, self.ws_ptr, self.ws_bytes, _stream_ptr(query.device))
@@ -782,7 +811,7 @@ class VarlenAttnPlan:
         if CHECK_ERRORS:
             self.check_errors()
             if merge is not None and merge.level_plan is not None:
-                merge.level_plan.check_errors()  # its combine records ran in this call
+                merge.level_plan.check_errors()  # its combine records (and chunk items) ran in this call
         return (out, lse) if return_lse else out
 
 

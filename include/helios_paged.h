@@ -242,17 +242,29 @@ int hx_varlen_attn_run_merged(const void* q, int64_t q_row_stride, int64_t q_hea
 /*
  * hx_varlen_attn_run_merged that also finishes the level batch's own run: the level
  * plan (level_batch, level_max_q, level_max_k, same heads and head_dim, its workspace
- * level_workspace) must have run its decode and chunk phases earlier on the same stream,
- * writing level_out / level_lse ([level_rows] rows, lse [n_q_heads, level_rows]); this
- * call runs that plan's combine phase (level_combine_hint bounds its records, as
- * combine_seqs_hint does for a run) before the merge reads the level rows. Its records
- * run as extra workgroups after the decode workgroups of this call's decode launch;
- * without a decode launch in this call, or for level rows of more than 8192 keys, they
- * get a combine launch of their own first. level_out and level_lse end
- * up with the bits of the level plan's own combine phase, and out / lse with the bits of
- * hx_varlen_attn_run_merged. Same requirements as hx_varlen_attn_run_merged; level_out
- * rows need 8-byte alignment (16-byte for the merge, as there). No reference
- * counterpart: it saves the cascade one dependent launch per layer.
+ * level_workspace) writes level_out / level_lse ([level_rows] rows, lse [n_q_heads,
+ * level_rows]). This call runs that plan's combine phase (level_combine_hint bounds its
+ * records, as combine_seqs_hint does for a run) before the merge reads the level rows.
+ * Its records run as extra workgroups after the decode workgroups of this call's decode
+ * launch; without a decode launch in this call, or for level rows of more than 8192
+ * keys, they get a combine launch of their own first.
+ *
+ * level_block_table == NULL: the level plan ran its decode and chunk phases earlier on
+ * the same stream. Otherwise this call runs the level plan's chunk phase as well, in one
+ * chunk launch with this call's own chunk items, ahead of the decode launch:
+ * level_block_table / level_block_table_stride are the level batch's block table,
+ * level_query_rows[level_query_rows_total] maps its packed rows to rows of q (as for
+ * hx_varlen_attn_run_rows), level_prefill_hint bounds its chunk items, and
+ * level_window_left / level_window_right are the window the level plan was built for
+ * (both ignored when level_block_table is NULL). The level
+ * plan must hold no decode rows (HX_WERR_GRID in its error word otherwise), and the call
+ * appends nothing: its own chunk rows then run before its decode launch.
+ *
+ * level_out and level_lse end up with the bits of the level plan's own run, and out / lse
+ * with the bits of hx_varlen_attn_run_merged. Same requirements as
+ * hx_varlen_attn_run_merged; level_out rows need 8-byte alignment (16-byte for the merge,
+ * as there). No reference counterpart: it saves the cascade one or two dependent launches
+ * per layer.
  */
 int hx_varlen_attn_run_cascade(const void* q, int64_t q_row_stride, int64_t q_head_stride,
                                const void* k_cache, const void* v_cache,
@@ -269,6 +281,9 @@ int hx_varlen_attn_run_cascade(const void* q, int64_t q_row_stride, int64_t q_he
                                float* level_lse, int64_t level_rows,
                                int32_t level_batch, int32_t level_max_q, int32_t level_max_k,
                                int32_t level_combine_hint, void* level_workspace, size_t level_workspace_bytes,
+                               const int32_t* level_block_table, int32_t level_block_table_stride,
+                               const int64_t* level_query_rows, int64_t level_query_rows_total,
+                               int32_t level_prefill_hint, int32_t level_window_left, int32_t level_window_right,
                                const int32_t* member_seq, const int32_t* member_of_seq, int32_t n_members,
                                const int32_t* part_start, const int32_t* part_idx, int32_t n_parts,
                                int32_t decode_items_hint, int32_t prefill_items_hint,

@@ -33,7 +33,7 @@ def test_loader_rejects_a_library_of_another_abi_version(monkeypatch):
 
 
 def test_abi_version_and_strerror():
-    assert _capi.lib().hx_abi_version() == _capi.ABI_VERSION == 5
+    assert _capi.lib().hx_abi_version() == _capi.ABI_VERSION == 6
     assert _capi.strerror(0) == "success"
     assert "invalid" in _capi.strerror(_capi.HX_E_INVALID_ARG)
     with pytest.raises(ValueError):
@@ -182,17 +182,20 @@ def test_cascade_run_rejects_a_bad_level_plan_on_the_host():
     """hx_varlen_attn_run_cascade checks the level plan's workspace and rows before any
     launch or device access (the pointers below are never dereferenced): a missing level
     workspace, one that is misaligned or too small for the level shape, and level rows
-    that are not 8-byte aligned are refused."""
+    that are not 8-byte aligned are refused; so is a level chunk run (a level block
+    table given) without its query row map or with a block-table width below 1."""
     lib = _capi.lib()
     mib = 1 << 20
 
-    def call(level_out=64 * mib, level_ws=128 * mib, level_ws_bytes=1 << 30):
+    def call(level_out=64 * mib, level_ws=128 * mib, level_ws_bytes=1 << 30, level_bt=None, level_bt_stride=0,
+             level_rows=None):
         return lib.hx_varlen_attn_run_cascade(
             16 * mib, 4096, 128, 32 * mib, 48 * mib, 1024, 128, 16, 256, 8 * mib, 4,
             2, 2, 1, 512, 32, 8, 128, 1 / math.sqrt(128), -1, 0, _capi.HX_DTYPE_BF16,
             96 * mib, 4096, 128, 112 * mib,
             level_out, 4096, 128, 120 * mib, 2,
             1, 2, 512, -1, level_ws, level_ws_bytes,
+            level_bt, level_bt_stride, level_rows, 2, -1, -1, -1,
             121 * mib, 122 * mib, 1, 123 * mib, 124 * mib, 1,
             -1, -1, -1, 256 * mib, 1 << 30, None)
 
@@ -200,6 +203,8 @@ def test_cascade_run_rejects_a_bad_level_plan_on_the_host():
     assert call(level_ws=128 * mib + 8) == _capi.HX_E_WORKSPACE
     assert call(level_ws_bytes=16) == _capi.HX_E_WORKSPACE
     assert call(level_out=64 * mib + 4) == _capi.HX_E_INVALID_ARG
+    assert call(level_bt=125 * mib, level_bt_stride=2) == _capi.HX_E_INVALID_ARG       # no row map
+    assert call(level_bt=125 * mib, level_bt_stride=0, level_rows=126 * mib) == _capi.HX_E_INVALID_ARG
 
 
 def test_noalloc_rejects_a_tick_beyond_its_scratch():

@@ -413,6 +413,53 @@ def test_level_combine_in_the_decode_launch(device, dtype, always_cascade, monke
     pb.run(q, kp, vp, cas.bt_b, return_lse=True, merge=merge_d)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_level_chunk_in_the_merging_call(device, dtype, always_cascade, monkeypatch):
+    """``MergeParts(level_plan=plan_a, level_block_table=..., level_query_rows=...)`` with
+    batch A not run at all: batch A's chunk items share batch B's chunk launch (ahead of
+    batch B's decode launch, which runs batch A's combine records). Batch A's rows and
+    log-sum-exps, and batch B's merged out and lse, equal batch A's full run followed by
+    the merging run, bit for bit; so does the cascade's attend, which takes this path."""
+    say("level batch's chunk items in batch B's chunk launch", dtype)
+    pool = _pool(device, pages=200, dtype=dtype)
+    cached = [8 * 256 + 5, 8 * 256 + 40, 8 * 256 + 300, 5000, 6100, 3 * 256 + 10, 7000, 2100, 600, 300]
+    _prefix, caches = _shared_caches(pool, cached, prefix_pages=8)
+    batch = PagedBatchCache(caches)
+    batch.prepare(1)
+    cas = batch._cascade
+    assert cas is not None
+    pa, pb = cas.plan_a, cas.plan_b
+    assert pa.hints[0] == 0 and pa.hints[1] > 0 and pa.hints[2] > 0, pa.hints
+    g = torch.Generator(device="cpu").manual_seed(11)
+    q = torch.randn((len(caches), 32, 128), generator=g).to(dtype).to(device)
+    kp, vp = pool.keys[0], pool.values[0]
+    rows_a, (_out_rows, part_start, part_idx) = cas.rows_a, cas.merge
+    member_seq, member_of_seq = cas.members
+    o_ref, lse_ref = pa.run(q, kp, vp, cas.bt_a, return_lse=True, query_rows=rows_a)
+    want, want_lse = pb.run(q, kp, vp, cas.bt_b, return_lse=True,
+                            merge=ops.MergeParts(o_ref, lse_ref, member_seq, member_of_seq, part_start, part_idx))
+    o_a = torch.full_like(o_ref, 7.0)
+    lse_a = torch.full_like(lse_ref, 3.0)
+    merge = ops.MergeParts(o_a, lse_a, member_seq, member_of_seq, part_start, part_idx, level_plan=pa,
+                           level_block_table=cas.bt_a, level_query_rows=rows_a)
+    got, got_lse = pb.run(q, kp, vp, cas.bt_b, return_lse=True, merge=merge)
+    out = cas.attend(q, kp, vp)
+    torch.cuda.synchronize()
+    assert pa.error_word() == 0 and pb.error_word() == 0
+    assert torch.equal(o_a, o_ref) and torch.equal(lse_a, lse_ref)
+    assert torch.equal(got, want) and torch.equal(got_lse, want_lse)
+    assert torch.equal(out, want)
+    with pytest.raises(ValueError, match="level_block_table"):
+        pb.run(q, kp, vp, cas.bt_b, return_lse=True, merge=merge._replace(level_block_table=None))
+    with pytest.raises(ValueError, match="three phases"):
+        pb.run(q, kp, vp, cas.bt_b, return_lse=True, merge=merge, phases=("decode", "combine"))
+    with pytest.raises(ValueError, match="level_query_rows"):
+        pb.run(q, kp, vp, cas.bt_b, return_lse=True, merge=merge._replace(level_query_rows=rows_a[:-1]))
+    # Checked mode reads both plans' error words after the call (and raises on neither).
+    monkeypatch.setattr(ops, "CHECK_ERRORS", True)
+    pb.run(q, kp, vp, cas.bt_b, return_lse=True, merge=merge)
+
+
 def test_level_combine_of_long_levels_gets_its_own_launch(device, always_cascade):
     """Levels longer than 8192 keys (40 shared pages here) want 512-thread combine
     workgroups, which a decode launch does not hold: batch A's records then get a combine
@@ -455,10 +502,20 @@ def test_level_combine_of_long_levels_gets_its_own_launch(device, always_cascade
     got, got_lse = pb.run(q, kp, vp, cas.bt_b, return_lse=True,
                           merge=ops.MergeParts(o_a, lse_a, member_seq, member_of_seq, part_start, part_idx,
                                                level_plan=pa))
+    # Batch A's chunk items in the merging call too (its records then get their launch
+    # between the shared chunk launch and batch B's decode launch).
+    o_f = torch.full_like(o_ref, 7.0)
+    lse_f = torch.full_like(lse_ref, 3.0)
+    got_f, got_lse_f = pb.run(q, kp, vp, cas.bt_b, return_lse=True,
+                              merge=ops.MergeParts(o_f, lse_f, member_seq, member_of_seq, part_start, part_idx,
+                                                   level_plan=pa, level_block_table=cas.bt_a,
+                                                   level_query_rows=rows_a))
     torch.cuda.synchronize()
     assert pa.error_word() == 0 and pb.error_word() == 0
     assert torch.equal(o_a, o_ref) and torch.equal(lse_a, lse_ref)
     assert torch.equal(got, want) and torch.equal(got_lse, want_lse)
+    assert torch.equal(o_f, o_ref) and torch.equal(lse_f, lse_ref)
+    assert torch.equal(got_f, want) and torch.equal(got_lse_f, want_lse)
     # And the attend path itself against the oracle.
     out = cas.attend(q, kp, vp)
     _compare(out.float().cpu().numpy(), _oracle(pool, caches, [1] * len(caches), q), "cascade attend, 40-page levels")
